@@ -1,0 +1,122 @@
+"""ctypes binding of ``libbitnet_hip.so`` (declarations: ``include/bitnet_hip.h``).
+
+The library is built in-tree by ``bitnetrs_amd/csrc/Makefile`` (see
+``bitnetrs_amd.build``).  Loading fails loudly when it is missing: there is
+no CPU fallback anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libbitnet_hip.so")
+CSRC = os.path.join(PKG_DIR, "csrc")
+HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "bitnet_hip.h")
+
+BNR_OK = 0
+BNR_INVALID_SHAPE = 1
+BNR_INVALID_CONFIG = 2
+BNR_BACKEND_ERROR = 3
+BNR_UNSUPPORTED_DEVICE = 4
+
+BNR_MIRROR_INCREMENTAL = 0
+BNR_MIRROR_FULL = 1
+
+
+class BitNetError(Exception):
+    """Mirror of bitnet_core::error::BitNetError (bitnet-core/src/error.rs:12-55)."""
+
+    kind = -1
+
+
+class InvalidShape(BitNetError):
+    kind = BNR_INVALID_SHAPE
+
+
+class InvalidConfig(BitNetError):
+    kind = BNR_INVALID_CONFIG
+
+
+class BackendError(BitNetError):
+    kind = BNR_BACKEND_ERROR
+
+
+class UnsupportedDevice(BitNetError):
+    kind = BNR_UNSUPPORTED_DEVICE
+
+
+ERRORS = {
+    BNR_INVALID_SHAPE: InvalidShape,
+    BNR_INVALID_CONFIG: InvalidConfig,
+    BNR_BACKEND_ERROR: BackendError,
+    BNR_UNSUPPORTED_DEVICE: UnsupportedDevice,
+}
+
+
+def build(verbose: bool = False) -> str:
+    """Compile libbitnet_hip.so for gfx950 with hipcc (works without a GPU)."""
+    out = None if verbose else subprocess.DEVNULL
+    subprocess.run(["make", "-B", "-s", "-C", CSRC], check=True, stdout=out)
+    return LIB_PATH
+
+
+_c = ctypes
+_f = _c.POINTER(_c.c_float)
+_sz = _c.c_size_t
+_vp = _c.c_void_p
+_i32p = _c.POINTER(_c.c_int32)
+
+# name -> (restype, argtypes); one entry per function in include/bitnet_hip.h
+SIGNATURES = {
+    "bnr_last_error": (_c.c_char_p, []),
+    "bnr_abi_version": (_c.c_uint32, []),
+    "bnr_create": (_c.c_int, [_c.c_int, _c.POINTER(_vp)]),
+    "bnr_destroy": (None, [_vp]),
+    "bnr_device_name": (_c.c_char_p, [_vp]),
+    "bnr_rope_embed": (_c.c_int, [_vp, _f, _sz, _f, _sz, _sz, _sz, _sz, _sz, _c.c_float]),
+    "bnr_masked_attention": (_c.c_int, [_vp, _f, _sz, _f, _sz, _f, _sz, _f, _sz, _sz, _sz, _sz,
+                                        _sz]),
+    "bnr_set_mirror_mode": (_c.c_int, [_vp, _c.c_int]),
+    "bnr_mirror_invalidate": (_c.c_int, [_vp]),
+    "bnr_dev_rope_append": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _c.c_float,
+                                       _vp, _vp, _sz, _vp]),
+    "bnr_dev_decode_attention": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                                            _vp]),
+    "bnr_dev_decode_step": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _c.c_float, _vp,
+                                       _vp, _sz, _vp, _vp, _vp, _vp]),
+    "bnr_dev_decode_step_batched": (_c.c_int, [_vp, _vp, _vp, _vp, _i32p, _sz, _sz, _sz, _sz,
+                                               _c.c_float, _vp, _vp, _sz, _vp, _vp]),
+    "bnr_dev_prefill_attention": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
+                                             _sz, _vp]),
+    "bnr_dev_prefill": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _c.c_float, _vp,
+                                   _vp, _sz, _vp, _vp]),
+    "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C {CSRC}` "
+                "(or __graft_entry__.build()); there is no fallback path")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    """Raise the BitNetError subclass for a non-zero status."""
+    if status != BNR_OK:
+        msg = load().bnr_last_error().decode()
+        raise ERRORS.get(status, BitNetError)(msg)

@@ -1,0 +1,205 @@
+"""Host-side mirror of the reference's Backend trait for the attention path.
+
+``HipBackend`` exposes the two trait methods this library replaces,
+``rope_embed`` (bitnet-core/src/backend/mod.rs:251-260) and
+``masked_attention`` (mod.rs:301-311), with the trait's argument order,
+in-place semantics and error kinds (``InvalidShape`` / ``InvalidConfig`` /
+``BackendError``), plus the device-pointer entry points of the C ABI that
+keep the KV cache resident in HBM.  All compute runs in libbitnet_hip.so on
+the GPU; nothing here computes on the CPU.
+
+Device entry points take ``torch`` CUDA tensors only as device memory; the
+library sees raw pointers and the current HIP stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import (BNR_MIRROR_FULL, BNR_MIRROR_INCREMENTAL, BackendError, BitNetError,
+                   InvalidConfig, InvalidShape, UnsupportedDevice)
+
+__all__ = ["HipBackend", "DeviceKVCache", "BitNetError", "InvalidShape", "InvalidConfig",
+           "BackendError", "UnsupportedDevice", "BNR_MIRROR_FULL", "BNR_MIRROR_INCREMENTAL"]
+
+_fp = ctypes.POINTER(ctypes.c_float)
+
+
+def _host(a: np.ndarray, name: str):
+    if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError(f"{name} must be a C-contiguous float32 numpy array")
+    return a.ctypes.data_as(_fp) if a.size else _fp()
+
+
+def _dev(t, name: str, allow_none: bool = False):
+    if t is None:
+        if allow_none:
+            return None
+        raise TypeError(f"{name} is required")
+    import torch
+
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32
+            and t.is_contiguous()):
+        raise TypeError(f"{name} must be a contiguous float32 CUDA tensor")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if isinstance(stream, int):
+        return ctypes.c_void_p(stream)
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class HipBackend:
+    """The HIP backend: CudaBackend's shape (bitnet-gpu-cuda/src/lib.rs:83-272)
+    with rope_embed / masked_attention implemented on gfx950."""
+
+    def __init__(self, device_id: int = 0):
+        self._L = _lib.load()
+        h = ctypes.c_void_p()
+        _lib.check(self._L.bnr_create(int(device_id), ctypes.byref(h)))
+        self._h = h
+        self.device_id = device_id
+
+    # lifecycle ------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.bnr_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def device_name(self) -> str:
+        return self._L.bnr_device_name(self._h).decode()
+
+    # trait-shaped host entry points ----------------------------------------
+    def rope_embed(self, q: np.ndarray, k: np.ndarray, position: int, head_dim: int,
+                   n_heads: int, n_kv_heads: int, theta: float) -> None:
+        """Backend::rope_embed: rotate q [n_heads*d] and k [n_kv_heads*d] in place."""
+        _lib.check(self._L.bnr_rope_embed(self._h, _host(q, "q"), q.size, _host(k, "k"), k.size,
+                                          position, head_dim, n_heads, n_kv_heads, theta))
+
+    def masked_attention(self, q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray,
+                         output: np.ndarray, n_heads: int, n_kv_heads: int, head_dim: int,
+                         cur_pos: int) -> None:
+        """Backend::masked_attention over head-major host caches; output overwritten."""
+        _lib.check(self._L.bnr_masked_attention(
+            self._h, _host(q, "q"), q.size, _host(k_cache, "k_cache"), k_cache.size,
+            _host(v_cache, "v_cache"), v_cache.size, _host(output, "output"), output.size,
+            n_heads, n_kv_heads, head_dim, cur_pos))
+
+    def set_mirror_mode(self, mode: int) -> None:
+        _lib.check(self._L.bnr_set_mirror_mode(self._h, mode))
+
+    def mirror_invalidate(self) -> None:
+        _lib.check(self._L.bnr_mirror_invalidate(self._h))
+
+    # device entry points ---------------------------------------------------
+    def dev_rope_append(self, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim, theta,
+                        k_cache, v_cache, cap, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_rope_append(
+            self._h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_tokens, start_pos, n_heads,
+            n_kv_heads, head_dim, theta, _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _stream(stream)))
+
+    def dev_decode_attention(self, q, k_cache, v_cache, cap, out, n_heads, n_kv_heads, head_dim,
+                             cur_pos, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_decode_attention(
+            self._h, _dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _dev(out, "out"), n_heads, n_kv_heads, head_dim, cur_pos, _stream(stream)))
+
+    def dev_decode_step(self, q, k, v, position, n_heads, n_kv_heads, head_dim, theta, k_cache,
+                        v_cache, cap, out, q_rot=None, k_rot=None, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_decode_step(
+            self._h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), position, n_heads, n_kv_heads,
+            head_dim, theta, _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _dev(out, "out"), _dev(q_rot, "q_rot", True), _dev(k_rot, "k_rot", True),
+            _stream(stream)))
+
+    def dev_decode_step_batched(self, q, k, v, positions, n_heads, n_kv_heads, head_dim, theta,
+                                k_caches, v_caches, cap, out, stream=None) -> None:
+        pos = np.ascontiguousarray(np.asarray(positions, dtype=np.int32))
+        _lib.check(self._L.bnr_dev_decode_step_batched(
+            self._h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"),
+            pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), pos.size, n_heads, n_kv_heads,
+            head_dim, theta, _dev(k_caches, "k_caches"), _dev(v_caches, "v_caches"), cap,
+            _dev(out, "out"), _stream(stream)))
+
+    def dev_prefill_attention(self, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
+                              n_kv_heads, head_dim, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_prefill_attention(
+            self._h, _dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _dev(out, "out"), n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
+            _stream(stream)))
+
+    def dev_prefill(self, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim, theta,
+                    k_cache, v_cache, cap, out, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_prefill(
+            self._h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_tokens, start_pos, n_heads,
+            n_kv_heads, head_dim, theta, _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _dev(out, "out"), _stream(stream)))
+
+    def dev_synchronize(self, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_synchronize(self._h, _stream(stream)))
+
+
+class DeviceKVCache:
+    """HBM-resident KV cache with KVCache's bookkeeping (bitnet-model/src/lib.rs:
+    118-292): per layer, head-major ``[n_kv_heads, max_seq, head_dim]`` K and V
+    buffers, per-layer lengths and ``filled_positions``."""
+
+    def __init__(self, n_layers: int, n_kv_heads: int, head_dim: int, max_seq: int,
+                 device: str = "cuda"):
+        import torch
+
+        self.n_layers, self.n_kv_heads, self.head_dim, self.max_seq = (
+            n_layers, n_kv_heads, head_dim, max_seq)
+        shape = (n_kv_heads, max_seq, head_dim)
+        self.k = [torch.zeros(shape, dtype=torch.float32, device=device) for _ in range(n_layers)]
+        self.v = [torch.zeros(shape, dtype=torch.float32, device=device) for _ in range(n_layers)]
+        self.layer_lengths = [0] * n_layers
+        self.filled_positions = 0
+
+    def check_store(self, layer: int, position: int, n_tokens: int = 1) -> None:
+        """store_kv's position rules (lib.rs:209-216) for n_tokens rows from position."""
+        last = position + n_tokens - 1
+        if last >= self.max_seq:
+            raise InvalidShape(f"invalid tensor shape: expected position < max_seq "
+                               f"({self.max_seq}), got position = {last}")
+        if position > self.layer_lengths[layer]:
+            raise InvalidShape(f"invalid tensor shape: expected position <= layer_len_positions "
+                               f"({self.layer_lengths[layer]}), got position = {position}")
+
+    def mark_stored(self, layer: int, position: int, n_tokens: int = 1) -> None:
+        self.layer_lengths[layer] = max(self.layer_lengths[layer], position + n_tokens)
+
+    def advance(self, n: int = 1) -> None:
+        if self.filled_positions + n > self.max_seq:
+            raise BackendError(f"KVCache::advance overflow: filled_positions="
+                               f"{self.filled_positions} max_seq={self.max_seq}")
+        self.filled_positions += n
+
+    def clear(self) -> None:
+        for t in self.k + self.v:
+            t.zero_()
+        self.layer_lengths = [0] * self.n_layers
+        self.filled_positions = 0
+
+    def __len__(self) -> int:
+        return self.filled_positions

@@ -1,0 +1,842 @@
+// bnr_api.cpp -- C ABI of the gfx950 GQA attention path (include/bitnet_hip.h).
+//
+// This is the host side of the backend: argument validation in the
+// reference's order and with its error kinds, the lazily built RoPE table,
+// the HBM mirrors of host KV caches behind the trait-shaped entry points,
+// the split-K decode planner and the workspace.  Kernels live in
+// bnr_kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/bitnet_hip.h"
+#include "bnr_internal.h"
+
+using namespace bnr;
+
+// ---------------------------------------------------------------------------
+// Errors: thread-local message, text as BitNetError's Display
+// (bitnet-core/src/error.rs:12-55).
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+static int set_ok() {
+  g_err.clear();
+  return BNR_OK;
+}
+
+static int err_shape(const std::string &expected, const std::string &got) {
+  g_err = "invalid tensor shape: expected " + expected + ", got " + got;
+  return BNR_INVALID_SHAPE;
+}
+
+static std::string fmt(const char *f, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, f);
+  vsnprintf(buf, sizeof buf, f, ap);
+  va_end(ap);
+  return buf;
+}
+
+static int err_config(const std::string &msg) {
+  g_err = "invalid model configuration: " + msg;
+  return BNR_INVALID_CONFIG;
+}
+
+static int err_backend(const std::string &msg) {
+  g_err = "backend error (HIP): " + msg;
+  return BNR_BACKEND_ERROR;
+}
+
+static int err_hip(hipError_t e, const char *what) {
+  return err_backend(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                 \
+  do {                                      \
+    hipError_t e_ = (expr);                 \
+    if (e_ != hipSuccess) return err_hip(e_, what); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+namespace {
+
+// HBM copy of one host KV cache (one layer), for bnr_masked_attention.
+struct Mirror {
+  const float *hk = nullptr, *hv = nullptr;
+  size_t k_len = 0, v_len = 0, n_kv = 0, head_dim = 0;
+  size_t rows = 0;    // rows per kv head held on the device
+  size_t synced = 0;  // rows 0..synced-1 match the host
+  float *dk = nullptr, *dv = nullptr;
+};
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+constexpr size_t kMaxMirrors = 256;
+
+}  // namespace
+
+struct bnr_ctx {
+  int device = 0;
+  std::string name;
+  std::mutex mu;
+  hipStream_t stream = nullptr;  // stream of the synchronous host entry points
+
+  // RoPE table (CpuBackend::rope_cache policy, bitnet-cpu/src/lib.rs:79,299-311)
+  bool tab_valid = false;
+  size_t tab_len = 0, tab_head_dim = 0;
+  float tab_theta = 0.f;
+  float *d_cos = nullptr, *d_sin = nullptr;
+
+  // workspace
+  float *ws_o = nullptr;
+  size_t ws_o_floats = 0;
+  float2 *ws_ml = nullptr;
+  size_t ws_ml_n = 0;
+  unsigned *counters = nullptr;
+  size_t n_counters = 0;
+  float *scratch = nullptr;  // generic-kernel scores and host-path staging
+  size_t scratch_floats = 0;
+
+  // host-path staging
+  float *d_q = nullptr, *d_k = nullptr, *d_out = nullptr;
+  size_t d_q_n = 0, d_k_n = 0, d_out_n = 0;
+
+  // mirrors, most recently used first
+  std::list<Mirror> mirrors;
+  int mirror_mode = BNR_MIRROR_INCREMENTAL;
+
+  // decode planner
+  int target_wgs = 640;
+  int force_rpg = 0;
+};
+
+namespace {
+
+void free_mirror(Mirror &m) {
+  if (m.dk) (void)hipFree(m.dk);
+  if (m.dv) (void)hipFree(m.dv);
+  m.dk = m.dv = nullptr;
+}
+
+// Grow-only device buffer.
+int ensure_buf(float **p, size_t *cap, size_t n, const char *what) {
+  if (*cap >= n && *p) return BNR_OK;
+  if (*p) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+  }
+  size_t want = std::max<size_t>(n, 1024);
+  HIP_TRY(hipMalloc((void **)p, want * sizeof(float)), what);
+  *cap = want;
+  return BNR_OK;
+}
+
+int ensure_counters(bnr_ctx *c, size_t n) {
+  if (c->n_counters >= n && c->counters) return BNR_OK;
+  if (c->counters) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(c->counters);
+    c->counters = nullptr;
+  }
+  size_t want = std::max<size_t>(n, 4096);
+  HIP_TRY(hipMalloc((void **)&c->counters, want * sizeof(unsigned)), "counter alloc");
+  HIP_TRY(hipMemset(c->counters, 0, want * sizeof(unsigned)), "counter clear");
+  HIP_TRY(hipDeviceSynchronize(), "counter clear");
+  c->n_counters = want;
+  return BNR_OK;
+}
+
+int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
+  int st = ensure_buf(&c->ws_o, &c->ws_o_floats, o_floats, "workspace alloc");
+  if (st) return st;
+  if (c->ws_ml_n < ml_n || !c->ws_ml) {
+    if (c->ws_ml) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(c->ws_ml);
+      c->ws_ml = nullptr;
+    }
+    size_t want = std::max<size_t>(ml_n, 1024);
+    HIP_TRY(hipMalloc((void **)&c->ws_ml, want * sizeof(float2)), "workspace alloc");
+    c->ws_ml_n = want;
+  }
+  return BNR_OK;
+}
+
+// RopeCache::new (bitnet-cpu/src/rope.rs:100-153) on the host: same f32
+// formula, same libm, so the table is bit-identical to the reference's.
+int build_table(bnr_ctx *c, size_t max_seq, size_t head_dim, float theta) {
+  if (head_dim == 0 || head_dim % 2 != 0)
+    return err_config(fmt("head_dim must be even and > 0, got %zu", head_dim));
+  if (!(theta > 0.0f) || !std::isfinite(theta))
+    return err_config(fmt("theta must be finite and > 0, got %g", (double)theta));
+  const size_t half = head_dim / 2, n = max_seq * half;
+  std::vector<float> hc(n), hs(n);
+  for (size_t pos = 0; pos < max_seq; ++pos) {
+    for (size_t i = 0; i < half; ++i) {
+      volatile float exponent = -2.0f * (float)i / (float)head_dim;
+      float freq = powf(theta, exponent);
+      volatile float angle = (float)pos * freq;
+      hc[pos * half + i] = cosf(angle);
+      hs[pos * half + i] = sinf(angle);
+    }
+  }
+  float *dc = nullptr, *ds = nullptr;
+  HIP_TRY(hipMalloc((void **)&dc, std::max<size_t>(n, 1) * sizeof(float)), "rope table alloc");
+  hipError_t e = hipMalloc((void **)&ds, std::max<size_t>(n, 1) * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipFree(dc);
+    return err_hip(e, "rope table alloc");
+  }
+  e = hipMemcpy(dc, hc.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(ds, hs.data(), n * sizeof(float), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(dc);
+    (void)hipFree(ds);
+    return err_hip(e, "rope table upload");
+  }
+  if (c->d_cos) {
+    (void)hipDeviceSynchronize();  // kernels in flight may still read the old table
+    (void)hipFree(c->d_cos);
+    (void)hipFree(c->d_sin);
+  }
+  c->d_cos = dc;
+  c->d_sin = ds;
+  c->tab_len = max_seq;
+  c->tab_head_dim = head_dim;
+  c->tab_theta = theta;
+  c->tab_valid = true;
+  return BNR_OK;
+}
+
+// CpuBackend::rope_embed's rebuild rule (bitnet-cpu/src/lib.rs:300-311).
+int ensure_table(bnr_ctx *c, size_t position, size_t head_dim, float theta) {
+  const bool reinit = !c->tab_valid || c->tab_head_dim != head_dim ||
+                      std::fabs(c->tab_theta - theta) > 1e-3f || position >= c->tab_len;
+  if (!reinit) return BNR_OK;
+  return build_table(c, std::max<size_t>(position + 1, 4096), head_dim, theta);
+}
+
+bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
+  if (head_dim != (size_t)kHeadDim || n_kv == 0 || n_kv > 64) return false;
+  const size_t g = n_heads / n_kv;
+  return g == 1 || g == 2 || g == 4;
+}
+
+// Split-K plan: rows per 16-lane row group (RPG) and passes so that the grid
+// has about target_wgs workgroups and at most kMaxSplits splits per
+// (sequence, kv head).
+void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeArgs &a) {
+  static const int rpgs[4] = {8, 4, 2, 1};
+  int rpg = 1;
+  if (c->force_rpg) {
+    rpg = c->force_rpg;
+  } else {
+    for (int r : rpgs) {
+      long long wgs = 0;
+      for (int b = 0; b < batch; ++b) wgs += (lens[b] + 16 * r - 1) / (16 * r);
+      if (wgs * n_kv >= c->target_wgs) {
+        rpg = r;
+        break;
+      }
+    }
+  }
+  int max_chunks = 0;
+  for (int b = 0; b < batch; ++b) max_chunks = std::max(max_chunks, (lens[b] + 16 * rpg - 1) / (16 * rpg));
+  const int passes = std::max(1, (max_chunks + kMaxSplits - 1) / kMaxSplits);
+  const int rows = 16 * rpg * passes;
+  a.rpg = rpg;
+  a.passes = passes;
+  a.rows_per_split = rows;
+  a.batch = batch;
+  a.split_off[0] = 0;
+  for (int b = 0; b < batch; ++b) a.split_off[b + 1] = a.split_off[b] + (lens[b] + rows - 1) / rows;
+}
+
+// Launch the fast decode kernel over `batch` (<= kMaxBatchPerLaunch)
+// sequences; a.{q,k_new,...,strides} are filled by the caller.
+int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n_kv, int group,
+               hipStream_t s) {
+  int lens[kMaxBatchPerLaunch];
+  for (int b = 0; b < batch; ++b) {
+    lens[b] = positions[b] + 1;
+    a.positions[b] = positions[b];
+  }
+  plan_decode(c, lens, batch, n_kv, a);
+  a.n_kv = n_kv;
+  a.group = group;
+  a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
+  const size_t splits = (size_t)a.split_off[batch];
+  int st = ensure_ws(c, splits * n_kv * group * kHeadDim, splits * n_kv * group);
+  if (st) return st;
+  st = ensure_counters(c, (size_t)batch * n_kv);
+  if (st) return st;
+  a.ws_o = c->ws_o;
+  a.ws_ml = c->ws_ml;
+  a.counters = c->counters;
+  HIP_TRY(launch_decode(a, s), "decode launch");
+  return BNR_OK;
+}
+
+int run_generic(bnr_ctx *c, const float *dq, const float *dk, const float *dv, long long kv_stride,
+                float *dout, size_t n_heads, size_t n_kv, size_t head_dim, size_t cur_pos,
+                hipStream_t s) {
+  const size_t L = cur_pos + 1;
+  int st = ensure_buf(&c->scratch, &c->scratch_floats, n_heads * L, "scratch alloc");
+  if (st) return st;
+  DecodeGenericArgs g{};
+  g.q = dq;
+  g.k_cache = dk;
+  g.v_cache = dv;
+  g.kv_stride = kv_stride;
+  g.out = dout;
+  g.scores = c->scratch;
+  g.n_heads = (int)n_heads;
+  g.group = (int)(n_heads / n_kv);
+  g.head_dim = (int)head_dim;
+  g.L = (int)L;
+  g.scale = 1.0f / sqrtf((float)head_dim);
+  HIP_TRY(launch_decode_generic(g, s), "decode launch");
+  return BNR_OK;
+}
+
+Mirror *find_mirror(bnr_ctx *c, const float *hk, size_t k_len, const float *hv, size_t v_len,
+                    size_t n_kv, size_t head_dim) {
+  for (auto it = c->mirrors.begin(); it != c->mirrors.end(); ++it) {
+    if (it->hk == hk && it->hv == hv && it->k_len == k_len && it->v_len == v_len &&
+        it->n_kv == n_kv && it->head_dim == head_dim) {
+      c->mirrors.splice(c->mirrors.begin(), c->mirrors, it);
+      return &c->mirrors.front();
+    }
+  }
+  return nullptr;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Lifecycle
+// ---------------------------------------------------------------------------
+extern "C" const char *bnr_last_error(void) { return g_err.c_str(); }
+
+extern "C" uint32_t bnr_abi_version(void) { return (1u << 16) | 0u; }
+
+extern "C" int bnr_create(int device_id, bnr_ctx **out) {
+  if (!out) return err_backend("bnr_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    g_err = "unsupported device: no HIP device available";
+    return BNR_UNSUPPORTED_DEVICE;
+  }
+  if (device_id < 0 || device_id >= n) {
+    g_err = fmt("unsupported device: HIP device %d does not exist (%d present)", device_id, n);
+    return BNR_UNSUPPORTED_DEVICE;
+  }
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, device_id), "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    g_err = fmt("unsupported device: HIP device %d is %s, this library is built for gfx950",
+                device_id, prop.gcnArchName);
+    return BNR_UNSUPPORTED_DEVICE;
+  }
+  DeviceGuard dg(device_id);
+  bnr_ctx *c = new bnr_ctx();
+  c->device = device_id;
+  c->name = fmt("HIP (%s, %s, device %d)", prop.name, prop.gcnArchName, device_id);
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return err_hip(e, "hipStreamCreate");
+  }
+  if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
+  if (const char *v = std::getenv("BNR_DECODE_RPG")) {
+    int r = atoi(v);
+    if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;
+  }
+  *out = c;
+  return set_ok();
+}
+
+extern "C" void bnr_destroy(bnr_ctx *c) {
+  if (!c) return;
+  {
+    std::lock_guard<std::mutex> lk(c->mu);
+    DeviceGuard dg(c->device);
+    (void)hipDeviceSynchronize();
+    for (auto &m : c->mirrors) free_mirror(m);
+    float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out};
+    for (float *p : bufs)
+      if (p) (void)hipFree(p);
+    if (c->ws_ml) (void)hipFree(c->ws_ml);
+    if (c->counters) (void)hipFree(c->counters);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+  }
+  delete c;
+}
+
+extern "C" const char *bnr_device_name(const bnr_ctx *c) { return c ? c->name.c_str() : ""; }
+
+// ---------------------------------------------------------------------------
+// Trait-shaped host entry points
+// ---------------------------------------------------------------------------
+extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size_t k_len,
+                              size_t position, size_t head_dim, size_t n_heads,
+                              size_t n_kv_heads, float theta) {
+  if (!c) return err_backend("context is NULL");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  // CpuBackend::rope_embed: table policy first (lib.rs:299-311), then
+  // apply_rope_cached's length checks (rope.rs:324-337).
+  int st = ensure_table(c, position, head_dim, theta);
+  if (st) return st;
+  const size_t hd = c->tab_head_dim;
+  if (q_len != n_heads * hd)
+    return err_shape(fmt("q.len() == %zu * %zu = %zu", n_heads, hd, n_heads * hd),
+                     fmt("q.len() = %zu", q_len));
+  if (k_len != n_kv_heads * hd)
+    return err_shape(fmt("k.len() == %zu * %zu = %zu", n_kv_heads, hd, n_kv_heads * hd),
+                     fmt("k.len() = %zu", k_len));
+  if (q_len + k_len == 0) return set_ok();
+  if ((q_len && !q) || (k_len && !k)) return err_backend("rope_embed: NULL slice");
+  st = ensure_buf(&c->d_q, &c->d_q_n, q_len + 1, "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_k, &c->d_k_n, k_len + 1, "staging alloc");
+  if (st) return st;
+  if (q_len) HIP_TRY(hipMemcpyAsync(c->d_q, q, q_len * 4, hipMemcpyHostToDevice, c->stream), "upload q");
+  if (k_len) HIP_TRY(hipMemcpyAsync(c->d_k, k, k_len * 4, hipMemcpyHostToDevice, c->stream), "upload k");
+  RopeAppendArgs a{};
+  a.q = c->d_q;
+  a.k = c->d_k;
+  a.n_tokens = 1;
+  a.start_pos = (int)position;
+  a.n_heads = (int)n_heads;
+  a.n_kv = (int)n_kv_heads;
+  a.head_dim = (int)hd;
+  a.cos_tab = c->d_cos;
+  a.sin_tab = c->d_sin;
+  HIP_TRY(launch_rope_append(a, c->stream), "rope launch");
+  if (q_len) HIP_TRY(hipMemcpyAsync(q, c->d_q, q_len * 4, hipMemcpyDeviceToHost, c->stream), "download q");
+  if (k_len) HIP_TRY(hipMemcpyAsync(k, c->d_k, k_len * 4, hipMemcpyDeviceToHost, c->stream), "download k");
+  HIP_TRY(hipStreamSynchronize(c->stream), "rope_embed");
+  return set_ok();
+}
+
+extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
+                                    const float *k_cache, size_t k_len, const float *v_cache,
+                                    size_t v_len, float *output, size_t out_len, size_t n_heads,
+                                    size_t n_kv_heads, size_t head_dim, size_t cur_pos) {
+  if (!c) return err_backend("context is NULL");
+  // Validation order of attention::masked_attention (attention.rs:109-161).
+  if (head_dim == 0) return err_shape("head_dim > 0", "head_dim = 0");
+  if (n_kv_heads == 0) return err_config("n_kv_heads must be > 0");
+  if (n_heads == 0) return err_config("n_heads must be > 0");
+  if (n_heads % n_kv_heads != 0)
+    return err_config(fmt("n_heads (%zu) must be divisible by n_kv_heads (%zu)", n_heads, n_kv_heads));
+  const size_t seq_len = cur_pos + 1;
+  const size_t head_stride = k_len / n_kv_heads;
+  const size_t required = n_kv_heads * head_stride;
+  const size_t q_expected = n_heads * head_dim;
+  if (q_len != q_expected)
+    return err_shape(fmt("q.len() == n_heads * head_dim = %zu * %zu = %zu", n_heads, head_dim, q_expected),
+                     fmt("q.len() = %zu", q_len));
+  if (k_len < required)
+    return err_shape(fmt("k_cache.len() >= %zu", required), fmt("k_cache.len() = %zu", k_len));
+  if (v_len < required)
+    return err_shape(fmt("v_cache.len() >= %zu", required), fmt("v_cache.len() = %zu", v_len));
+  if (head_stride < seq_len * head_dim)
+    return err_shape(fmt("per-head cache stride >= %zu", seq_len * head_dim),
+                     fmt("per-head cache stride = %zu", head_stride));
+  if (out_len != q_expected)
+    return err_shape(fmt("output.len() == n_heads * head_dim = %zu", q_expected),
+                     fmt("output.len() = %zu", out_len));
+  if (!q || !k_cache || !v_cache || !output) return err_backend("masked_attention: NULL slice");
+
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+
+  // ---- HBM mirror of this layer's cache ----
+  const size_t rows = head_stride / head_dim;  // >= seq_len by the checks above
+  Mirror *m = find_mirror(c, k_cache, k_len, v_cache, v_len, n_kv_heads, head_dim);
+  if (!m) {
+    if (c->mirrors.size() >= kMaxMirrors) {
+      (void)hipStreamSynchronize(c->stream);
+      free_mirror(c->mirrors.back());
+      c->mirrors.pop_back();
+    }
+    Mirror nm;
+    nm.hk = k_cache;
+    nm.hv = v_cache;
+    nm.k_len = k_len;
+    nm.v_len = v_len;
+    nm.n_kv = n_kv_heads;
+    nm.head_dim = head_dim;
+    nm.rows = rows;
+    const size_t bytes = n_kv_heads * rows * head_dim * sizeof(float);
+    HIP_TRY(hipMalloc((void **)&nm.dk, bytes), "mirror alloc");
+    hipError_t e = hipMalloc((void **)&nm.dv, bytes);
+    if (e != hipSuccess) {
+      (void)hipFree(nm.dk);
+      return err_hip(e, "mirror alloc");
+    }
+    c->mirrors.push_front(nm);
+    m = &c->mirrors.front();
+  }
+  size_t r0 = 0;
+  if (c->mirror_mode == BNR_MIRROR_INCREMENTAL && m->synced == cur_pos) r0 = cur_pos;
+  const size_t dpitch = m->rows * head_dim * sizeof(float);
+  const size_t spitch = head_stride * sizeof(float);
+  const size_t width = (seq_len - r0) * head_dim * sizeof(float);
+  m->synced = 0;  // unknown until both copies succeed
+  HIP_TRY(hipMemcpy2DAsync(m->dk + r0 * head_dim, dpitch, k_cache + r0 * head_dim, spitch, width,
+                           n_kv_heads, hipMemcpyHostToDevice, c->stream),
+          "mirror upload k");
+  HIP_TRY(hipMemcpy2DAsync(m->dv + r0 * head_dim, dpitch, v_cache + r0 * head_dim, spitch, width,
+                           n_kv_heads, hipMemcpyHostToDevice, c->stream),
+          "mirror upload v");
+  m->synced = seq_len;
+
+  int st = ensure_buf(&c->d_q, &c->d_q_n, q_len, "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_out, &c->d_out_n, out_len, "staging alloc");
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(c->d_q, q, q_len * 4, hipMemcpyHostToDevice, c->stream), "upload q");
+  const long long kv_stride = (long long)(m->rows * head_dim);
+  if (fast_shape(n_heads, n_kv_heads, head_dim)) {
+    DecodeArgs a{};
+    a.q = c->d_q;
+    a.k_cache = m->dk;
+    a.v_cache = m->dv;
+    a.kv_stride = kv_stride;
+    a.out = c->d_out;
+    const int p = (int)cur_pos;
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), c->stream);
+  } else {
+    st = run_generic(c, c->d_q, m->dk, m->dv, kv_stride, c->d_out, n_heads, n_kv_heads, head_dim,
+                     cur_pos, c->stream);
+  }
+  if (st) {
+    m->synced = 0;
+    return st;
+  }
+  HIP_TRY(hipMemcpyAsync(output, c->d_out, out_len * 4, hipMemcpyDeviceToHost, c->stream), "download out");
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    m->synced = 0;
+    return err_hip(e, "masked_attention");
+  }
+  return set_ok();
+}
+
+extern "C" int bnr_set_mirror_mode(bnr_ctx *c, int mode) {
+  if (!c) return err_backend("context is NULL");
+  if (mode != BNR_MIRROR_INCREMENTAL && mode != BNR_MIRROR_FULL)
+    return err_config(fmt("unknown mirror mode %d", mode));
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->mirror_mode = mode;
+  return set_ok();
+}
+
+extern "C" int bnr_mirror_invalidate(bnr_ctx *c) {
+  if (!c) return err_backend("context is NULL");
+  std::lock_guard<std::mutex> lk(c->mu);
+  for (auto &m : c->mirrors) m.synced = 0;
+  return set_ok();
+}
+
+// ---------------------------------------------------------------------------
+// Device entry points
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_heads(size_t n_heads, size_t n_kv, size_t head_dim) {
+  if (head_dim == 0) return err_shape("head_dim > 0", "head_dim = 0");
+  if (n_kv == 0) return err_config("n_kv_heads must be > 0");
+  if (n_heads == 0) return err_config("n_heads must be > 0");
+  if (n_heads % n_kv != 0)
+    return err_config(fmt("n_heads (%zu) must be divisible by n_kv_heads (%zu)", n_heads, n_kv));
+  return BNR_OK;
+}
+
+int check_rope(size_t head_dim, float theta) {
+  if (head_dim == 0 || head_dim % 2 != 0)
+    return err_config(fmt("head_dim must be even and > 0, got %zu", head_dim));
+  if (!(theta > 0.0f) || !std::isfinite(theta))
+    return err_config(fmt("theta must be finite and > 0, got %g", (double)theta));
+  return BNR_OK;
+}
+
+int check_rows(size_t last_pos, size_t cap) {
+  if (last_pos >= cap)
+    return err_shape(fmt("position < max_seq (%zu)", cap), fmt("position = %zu", last_pos));
+  return BNR_OK;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int launch_rope_append_dev(bnr_ctx *c, float *q, float *k, const float *v, size_t n_tokens,
+                           size_t start_pos, size_t n_heads, size_t n_kv, size_t head_dim,
+                           float *k_cache, float *v_cache, size_t cap, hipStream_t s) {
+  RopeAppendArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.n_tokens = (int)n_tokens;
+  a.start_pos = (int)start_pos;
+  a.n_heads = (int)n_heads;
+  a.n_kv = (int)n_kv;
+  a.head_dim = (int)head_dim;
+  a.cos_tab = c->d_cos;
+  a.sin_tab = c->d_sin;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.kv_stride = (long long)(cap * head_dim);
+  HIP_TRY(launch_rope_append(a, s), "rope/append launch");
+  return BNR_OK;
+}
+
+}  // namespace
+
+extern "C" int bnr_dev_rope_append(bnr_ctx *c, float *q, float *k, const float *v,
+                                   size_t n_tokens, size_t start_pos, size_t n_heads,
+                                   size_t n_kv_heads, size_t head_dim, float theta,
+                                   float *k_cache, float *v_cache, size_t cap, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rope(head_dim, theta);
+  if (st) return st;
+  if (n_tokens == 0) return set_ok();
+  st = check_rows(start_pos + n_tokens - 1, cap);
+  if (st) return st;
+  if (!q || !k || !v || !k_cache || !v_cache) return err_backend("rope_append: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  st = ensure_table(c, start_pos + n_tokens - 1, head_dim, theta);
+  if (st) return st;
+  st = launch_rope_append_dev(c, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
+                              k_cache, v_cache, cap, (hipStream_t)stream);
+  return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_decode_attention(bnr_ctx *c, const float *q, const float *k_cache,
+                                        const float *v_cache, size_t cap, float *out,
+                                        size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                        size_t cur_pos, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rows(cur_pos, cap);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !out) return err_backend("decode_attention: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  hipStream_t s = (hipStream_t)stream;
+  const long long kv_stride = (long long)(cap * head_dim);
+  if (fast_shape(n_heads, n_kv_heads, head_dim) && aligned16(q) && aligned16(k_cache) &&
+      aligned16(v_cache)) {
+    DecodeArgs a{};
+    a.q = q;
+    a.k_cache = const_cast<float *>(k_cache);
+    a.v_cache = const_cast<float *>(v_cache);
+    a.kv_stride = kv_stride;
+    a.out = out;
+    const int p = (int)cur_pos;
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+  } else {
+    st = run_generic(c, q, k_cache, v_cache, kv_stride, out, n_heads, n_kv_heads, head_dim, cur_pos, s);
+  }
+  return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_decode_step(bnr_ctx *c, const float *q, const float *k, const float *v,
+                                   size_t position, size_t n_heads, size_t n_kv_heads,
+                                   size_t head_dim, float theta, float *k_cache, float *v_cache,
+                                   size_t cap, float *out, float *q_rot, float *k_rot,
+                                   void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rope(head_dim, theta);
+  if (!st) st = check_rows(position, cap);
+  if (st) return st;
+  if (!q || !k || !v || !k_cache || !v_cache || !out) return err_backend("decode_step: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  st = ensure_table(c, position, head_dim, theta);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  const long long kv_stride = (long long)(cap * head_dim);
+  const bool al = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
+                  aligned16(v_cache) && (!q_rot || aligned16(q_rot)) && (!k_rot || aligned16(k_rot));
+  if (fast_shape(n_heads, n_kv_heads, head_dim) && al) {
+    DecodeArgs a{};
+    a.q = q;
+    a.k_new = k;
+    a.v_new = v;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.kv_stride = kv_stride;
+    a.out = out;
+    a.q_rot = q_rot;
+    a.k_rot = k_rot;
+    a.cos_tab = c->d_cos;
+    a.sin_tab = c->d_sin;
+    const int p = (int)position;
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+    return st ? st : set_ok();
+  }
+  // Any other shape: rotate copies, append, then the generic kernel.
+  const size_t qn = n_heads * head_dim, kn = n_kv_heads * head_dim;
+  float *qw = q_rot, *kw = k_rot;
+  st = ensure_buf(&c->d_k, &c->d_k_n, qn + kn, "staging alloc");
+  if (st) return st;
+  if (!qw) qw = c->d_k;
+  if (!kw) kw = c->d_k + qn;
+  HIP_TRY(hipMemcpyAsync(qw, q, qn * 4, hipMemcpyDeviceToDevice, s), "copy q");
+  HIP_TRY(hipMemcpyAsync(kw, k, kn * 4, hipMemcpyDeviceToDevice, s), "copy k");
+  st = launch_rope_append_dev(c, qw, kw, v, 1, position, n_heads, n_kv_heads, head_dim, k_cache,
+                              v_cache, cap, s);
+  if (!st) st = run_generic(c, qw, k_cache, v_cache, kv_stride, out, n_heads, n_kv_heads, head_dim,
+                            position, s);
+  return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_decode_step_batched(bnr_ctx *c, const float *q, const float *k,
+                                           const float *v, const int32_t *positions, size_t batch,
+                                           size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                           float theta, float *k_caches, float *v_caches,
+                                           size_t cap, float *out, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rope(head_dim, theta);
+  if (st) return st;
+  if (batch == 0) return set_ok();
+  if (!positions || !q || !k || !v || !k_caches || !v_caches || !out)
+    return err_backend("decode_step_batched: NULL pointer");
+  size_t maxp = 0;
+  for (size_t b = 0; b < batch; ++b) {
+    if (positions[b] < 0)
+      return err_shape("position >= 0", fmt("positions[%zu] = %d", b, positions[b]));
+    maxp = std::max(maxp, (size_t)positions[b]);
+  }
+  st = check_rows(maxp, cap);
+  if (st) return st;
+  if (!fast_shape(n_heads, n_kv_heads, head_dim))
+    return err_config(fmt("batched decode needs head_dim %d and n_heads/n_kv_heads in {1,2,4}, got "
+                          "head_dim %zu, n_heads %zu, n_kv_heads %zu",
+                          kHeadDim, head_dim, n_heads, n_kv_heads));
+  if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_caches) && aligned16(v_caches)))
+    return err_shape("16-byte aligned device pointers", "an unaligned pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  st = ensure_table(c, maxp, head_dim, theta);
+  if (st) return st;
+  hipStream_t s = (hipStream_t)stream;
+  const long long qs = (long long)(n_heads * head_dim), ks = (long long)(n_kv_heads * head_dim);
+  const long long cs = (long long)(n_kv_heads * cap * head_dim);
+  for (size_t b0 = 0; b0 < batch; b0 += kMaxBatchPerLaunch) {
+    const int nb = (int)std::min<size_t>(kMaxBatchPerLaunch, batch - b0);
+    DecodeArgs a{};
+    a.q = q + b0 * qs;
+    a.k_new = k + b0 * ks;
+    a.v_new = v + b0 * ks;
+    a.k_cache = k_caches + b0 * cs;
+    a.v_cache = v_caches + b0 * cs;
+    a.q_bstride = qs;
+    a.kn_bstride = ks;
+    a.cache_bstride = cs;
+    a.out_bstride = qs;
+    a.kv_stride = (long long)(cap * head_dim);
+    a.out = out + b0 * qs;
+    a.cos_tab = c->d_cos;
+    a.sin_tab = c->d_sin;
+    st = run_decode(c, a, positions + b0, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+    if (st) return st;
+  }
+  return set_ok();
+}
+
+extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float *k_cache,
+                                         const float *v_cache, size_t cap, float *out,
+                                         size_t n_tokens, size_t start_pos, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (st) return st;
+  if (n_tokens == 0) return set_ok();
+  st = check_rows(start_pos + n_tokens - 1, cap);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !out) return err_backend("prefill_attention: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  hipStream_t s = (hipStream_t)stream;
+  const long long qs = (long long)(n_heads * head_dim);
+  const long long kv_stride = (long long)(cap * head_dim);
+  if (fast_shape(n_heads, n_kv_heads, head_dim) && aligned16(q) && aligned16(k_cache) &&
+      aligned16(v_cache)) {
+    // Each query row is a decode over the shared cache at its own position.
+    int pos[kMaxBatchPerLaunch];
+    for (size_t t0 = 0; t0 < n_tokens; t0 += kMaxBatchPerLaunch) {
+      const int nb = (int)std::min<size_t>(kMaxBatchPerLaunch, n_tokens - t0);
+      for (int i = 0; i < nb; ++i) pos[i] = (int)(start_pos + t0 + i);
+      DecodeArgs a{};
+      a.q = q + t0 * qs;
+      a.k_cache = const_cast<float *>(k_cache);
+      a.v_cache = const_cast<float *>(v_cache);
+      a.q_bstride = qs;
+      a.out_bstride = qs;
+      a.kv_stride = kv_stride;
+      a.out = out + t0 * qs;
+      st = run_decode(c, a, pos, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+      if (st) return st;
+    }
+    return set_ok();
+  }
+  for (size_t i = 0; i < n_tokens; ++i) {
+    st = run_generic(c, q + i * qs, k_cache, v_cache, kv_stride, out + i * qs, n_heads, n_kv_heads,
+                     head_dim, start_pos + i, s);
+    if (st) return st;
+  }
+  return set_ok();
+}
+
+extern "C" int bnr_dev_prefill(bnr_ctx *c, float *q, float *k, const float *v, size_t n_tokens,
+                               size_t start_pos, size_t n_heads, size_t n_kv_heads,
+                               size_t head_dim, float theta, float *k_cache, float *v_cache,
+                               size_t cap, float *out, void *stream) {
+  int st = bnr_dev_rope_append(c, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
+                               theta, k_cache, v_cache, cap, stream);
+  if (st) return st;
+  return bnr_dev_prefill_attention(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
+                                   n_kv_heads, head_dim, stream);
+}
+
+extern "C" int bnr_dev_synchronize(bnr_ctx *c, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  DeviceGuard dg(c->device);
+  HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "synchronize");
+  return set_ok();
+}

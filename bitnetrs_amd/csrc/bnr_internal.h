@@ -1,0 +1,73 @@
+// bnr_internal.h -- launch interface between the C ABI layer (bnr_api.cpp)
+// and the gfx950 kernels (bnr_kernels.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace bnr {
+
+// Head dimension of the fast kernels (BitNet b1.58 2B: 2560 / 20).
+constexpr int kHeadDim = 128;
+// Sequences per decode launch: per-sequence positions and split offsets
+// travel in the kernel-argument segment, so no host->device copy is needed.
+constexpr int kMaxBatchPerLaunch = 64;
+// Upper bound on context splits per (sequence, kv head); longer contexts
+// give each workgroup several passes over its rows.
+constexpr int kMaxSplits = 256;
+
+// RoPE + append over n_tokens consecutive positions of one sequence.  q and
+// k are rotated in place; when k_cache is non-null the rotated k rows and the
+// v rows are written at rows start_pos + i of a head-major cache.
+struct RopeAppendArgs {
+  float *q;
+  float *k;
+  const float *v;
+  int n_tokens, start_pos, n_heads, n_kv, head_dim;
+  const float *cos_tab, *sin_tab;  // [table_len x head_dim/2]
+  float *k_cache, *v_cache;
+  long long kv_stride;  // elements between kv heads of the cache (cap * head_dim)
+};
+hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s);
+
+// Split-K decode attention for head_dim 128.  One workgroup owns one
+// (sequence, kv head, context chunk) and serves the kv head's G query
+// heads from one read of each K/V row.
+struct DecodeArgs {
+  const float *q;      // [b][n_kv*G][128]; raw when cos_tab != null
+  const float *k_new;  // [b][n_kv][128] raw new keys (fused append) or null
+  const float *v_new;  // [b][n_kv][128] new values (fused append) or null
+  float *k_cache, *v_cache;
+  long long q_bstride, kn_bstride, cache_bstride, out_bstride;  // elements
+  long long kv_stride;                                          // elements
+  float *out;
+  float *q_rot, *k_rot;           // optional rotated q / k outputs
+  const float *cos_tab, *sin_tab; // [table_len x 64] or null (q pre-rotated)
+  float *ws_o;                    // split partials: [split][n_kv][G][128]
+  float2 *ws_ml;                  // split (max, sum): [split][n_kv][G]
+  unsigned *counters;             // [batch][n_kv], zero between launches
+  float scale_log2;               // log2(e) / sqrt(128)
+  int n_kv, group, batch;
+  int rows_per_split;             // rows a workgroup owns (16*RPG*passes)
+  int rpg;                        // rows per 16-lane row group and pass
+  int passes;
+  int positions[kMaxBatchPerLaunch];
+  int split_off[kMaxBatchPerLaunch + 1];
+};
+hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
+
+// Any head_dim / group size: one workgroup per query head, scores staged in
+// a global workspace [n_heads][L].
+struct DecodeGenericArgs {
+  const float *q;
+  const float *k_cache, *v_cache;
+  long long kv_stride;
+  float *out;
+  float *scores;
+  int n_heads, group, head_dim, L;
+  float scale;
+};
+hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s);
+
+}  // namespace bnr

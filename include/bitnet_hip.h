@@ -1,0 +1,173 @@
+/*
+ * bitnet_hip.h -- C ABI of the MI355X (gfx950) GQA attention hot path of
+ * bitnetrs: RoPE (half-split, any theta) on Q/K, KV-cache append into an
+ * HBM-resident head-major cache, split-K decode attention and causal
+ * flash prefill.
+ *
+ * Conventions
+ *  - Every entry point returns an int status (BNR_OK == 0) and never aborts.
+ *    On failure, bnr_last_error() returns the calling thread's message; its
+ *    text follows BitNetError's Display strings
+ *    (bitnet-core/src/error.rs:12-55).
+ *  - "Host" entry points (bnr_rope_embed, bnr_masked_attention) take host
+ *    slices exactly as the reference's Backend trait methods do and are
+ *    synchronous: outputs are written when they return.
+ *  - "Device" entry points (bnr_dev_*) take device pointers (HBM), are
+ *    ordered on the given HIP stream (NULL = the legacy default stream) and
+ *    return as soon as the work is enqueued.  Calls that share one context
+ *    share its workspace: they must be issued on one stream, or serialised
+ *    by the caller.
+ *  - Tensors are fp32, row-major.  A KV cache of one layer is head-major
+ *    [n_kv_heads x cap x head_dim]: element (h, t, d) lives at
+ *    h*cap*head_dim + t*head_dim + d (Backend::masked_attention contract,
+ *    bitnet-core/src/backend/mod.rs:278-287; KVCache::store_kv,
+ *    bitnet-model/src/lib.rs:218-228).
+ */
+#ifndef BITNET_HIP_H
+#define BITNET_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes, one per BitNetError variant the path can return. */
+#define BNR_OK 0
+#define BNR_INVALID_SHAPE 1      /* BitNetError::InvalidShape            */
+#define BNR_INVALID_CONFIG 2     /* BitNetError::InvalidConfig           */
+#define BNR_BACKEND_ERROR 3      /* BitNetError::BackendError{"HIP",..}  */
+#define BNR_UNSUPPORTED_DEVICE 4 /* BitNetError::UnsupportedDevice       */
+
+typedef struct bnr_ctx bnr_ctx;
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char *bnr_last_error(void);
+
+/* ABI version of this header: (major << 16) | minor. */
+uint32_t bnr_abi_version(void);
+
+/* Create a backend bound to HIP device `device_id`; replaces
+ * CudaBackend::new(device_id) (bitnet-gpu-cuda/src/lib.rs:94-104).  Fails
+ * with BNR_UNSUPPORTED_DEVICE when the device does not exist or is not a
+ * gfx950 GPU. */
+int bnr_create(int device_id, bnr_ctx **out);
+/* Release every device buffer the context owns (mirrors, tables, workspace). */
+void bnr_destroy(bnr_ctx *ctx);
+/* Backend::device_name (bitnet-core/src/backend/mod.rs:511-516). */
+const char *bnr_device_name(const bnr_ctx *ctx);
+
+/* ----------------------------------------------------------------------- */
+/* Trait-shaped host entry points                                          */
+/* ----------------------------------------------------------------------- */
+
+/* Backend::rope_embed (bitnet-core/src/backend/mod.rs:251-260) as
+ * CpuBackend implements it (bitnet-cpu/src/lib.rs:289-314): q
+ * [n_heads*head_dim] and k [n_kv_heads*head_dim] are rotated in place at
+ * `position` with the half-split pairing (i, i+head_dim/2).  The cos/sin
+ * table is built on the host with the reference formula and kept in HBM;
+ * it is rebuilt when head_dim changes, |theta - cached| > 1e-3 or
+ * position >= its length (new length max(position+1, 4096)).  Errors:
+ * zero/odd head_dim or non-positive/non-finite theta -> INVALID_CONFIG;
+ * wrong q or k length -> INVALID_SHAPE. */
+int bnr_rope_embed(bnr_ctx *ctx, float *q, size_t q_len, float *k, size_t k_len,
+                   size_t position, size_t head_dim, size_t n_heads, size_t n_kv_heads,
+                   float theta);
+
+/* Backend::masked_attention (bitnet-core/src/backend/mod.rs:301-311) as
+ * attention::masked_attention implements it (bitnet-cpu/src/attention.rs:
+ * 97-209): out[h] = softmax(q_h . K[h/G, 0..=cur_pos] / sqrt(d)) V[h/G].
+ * cap is k_len / n_kv_heads / head_dim, as in the reference (attention.rs:
+ * 128).  The context keeps an HBM mirror of each host cache, keyed by
+ * (k_cache, v_cache, k_len): when the mirror holds exactly rows
+ * 0..cur_pos-1, only row cur_pos is uploaded; otherwise rows 0..=cur_pos
+ * are re-uploaded.  Validation order and error kinds follow attention.rs:
+ * 109-161. */
+int bnr_masked_attention(bnr_ctx *ctx, const float *q, size_t q_len, const float *k_cache,
+                         size_t k_len, const float *v_cache, size_t v_len, float *output,
+                         size_t out_len, size_t n_heads, size_t n_kv_heads,
+                         size_t head_dim, size_t cur_pos);
+
+/* Mirror policy of bnr_masked_attention. */
+#define BNR_MIRROR_INCREMENTAL 0 /* upload only the new row when in sync (default) */
+#define BNR_MIRROR_FULL 1        /* upload rows 0..=cur_pos on every call          */
+int bnr_set_mirror_mode(bnr_ctx *ctx, int mode);
+/* Forget every mirror (call after rewriting rows other than the newest). */
+int bnr_mirror_invalidate(bnr_ctx *ctx);
+
+/* ----------------------------------------------------------------------- */
+/* Device entry points (HBM-resident cache, stream-ordered)                */
+/* ----------------------------------------------------------------------- */
+
+/* RoPE + KV append for n_tokens consecutive tokens at positions
+ * start_pos .. start_pos+n_tokens-1 of one sequence: the per-token
+ * rope_embed + KVCache::store_kv pair of BitNetModel::forward
+ * (bitnet-model/src/lib.rs:684-699).  q [n_tokens x n_heads x d] and k
+ * [n_tokens x n_kv_heads x d] are rotated in place; rotated k rows and v
+ * rows are written into k_cache / v_cache rows.  Requires
+ * start_pos + n_tokens <= cap.  The rotation is bit-identical to the
+ * reference's (same table, unfused products). */
+int bnr_dev_rope_append(bnr_ctx *ctx, float *q, float *k, const float *v, size_t n_tokens,
+                        size_t start_pos, size_t n_heads, size_t n_kv_heads,
+                        size_t head_dim, float theta, float *k_cache, float *v_cache,
+                        size_t cap, void *stream);
+
+/* Decode attention of one token over cache rows 0..=cur_pos (q already
+ * rotated): the masked_attention call of forward_into's decode path
+ * (bitnet-model/src/lib.rs:1022-1036).  out [n_heads x d]. */
+int bnr_dev_decode_attention(bnr_ctx *ctx, const float *q, const float *k_cache,
+                             const float *v_cache, size_t cap, float *out, size_t n_heads,
+                             size_t n_kv_heads, size_t head_dim, size_t cur_pos,
+                             void *stream);
+
+/* One fused decode step of one layer, in a single kernel launch: rotate q
+ * (raw, [n_heads x d]) and k (raw, [n_kv_heads x d]) at `position`, append
+ * the rotated k row and the v row at `position`, and attend over rows
+ * 0..=position.  q and k are not modified; if q_rot / k_rot are non-NULL
+ * the rotated vectors are written there (what rope_embed leaves in its
+ * in-place buffers).  Equivalent to rope_embed + store_kv + masked_attention
+ * (bitnet-model/src/lib.rs:1004-1036). */
+int bnr_dev_decode_step(bnr_ctx *ctx, const float *q, const float *k, const float *v,
+                        size_t position, size_t n_heads, size_t n_kv_heads,
+                        size_t head_dim, float theta, float *k_cache, float *v_cache,
+                        size_t cap, float *out, float *q_rot, float *k_rot, void *stream);
+
+/* Fused decode step for a batch of independent sequences with ragged
+ * lengths (no reference counterpart: the reference is single-sequence,
+ * bitnet-core/src/backend/mod.rs:301-311 applied per sequence).
+ * q [batch x n_heads x d], k/v [batch x n_kv_heads x d] raw projections;
+ * positions (HOST array, batch entries) gives each sequence's new-token
+ * position; caches are [batch x n_kv_heads x cap x d]; out
+ * [batch x n_heads x d]. */
+int bnr_dev_decode_step_batched(bnr_ctx *ctx, const float *q, const float *k,
+                                const float *v, const int32_t *positions, size_t batch,
+                                size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                float theta, float *k_caches, float *v_caches, size_t cap,
+                                float *out, void *stream);
+
+/* Causal prefill attention for n_tokens queries at positions
+ * start_pos .. start_pos+n_tokens-1 (q already rotated,
+ * [n_tokens x n_heads x d]); query i attends to cache rows
+ * 0..=start_pos+i, which must already hold the rotated keys.  Equivalent to
+ * n_tokens masked_attention calls in BitNetModel::forward's token loop
+ * (bitnet-model/src/lib.rs:702-718).  out [n_tokens x n_heads x d]. */
+int bnr_dev_prefill_attention(bnr_ctx *ctx, const float *q, const float *k_cache,
+                              const float *v_cache, size_t cap, float *out,
+                              size_t n_tokens, size_t start_pos, size_t n_heads,
+                              size_t n_kv_heads, size_t head_dim, void *stream);
+
+/* Full causal prefill of one layer: bnr_dev_rope_append followed by
+ * bnr_dev_prefill_attention (q and k are rotated in place). */
+int bnr_dev_prefill(bnr_ctx *ctx, float *q, float *k, const float *v, size_t n_tokens,
+                    size_t start_pos, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                    float theta, float *k_cache, float *v_cache, size_t cap, float *out,
+                    void *stream);
+
+/* Wait for all work the context enqueued on `stream`. */
+int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BITNET_HIP_H */

@@ -1,0 +1,556 @@
+/*
+ * bnr_oracle.c -- CPU restatement of bitnetrs's GQA attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the reported CPU baseline); the
+ * product library never links it.
+ *
+ * Build: gcc -O3 -mavx2 -mfma -ffp-contract=off -fopenmp (oracle/Makefile).
+ * -ffp-contract=off matters: rustc never fuses a*b+c, so the only fused
+ * multiply-adds are the explicit _mm256_fmadd_ps of the reference's AVX2
+ * kernels.  Transcendentals are glibc powf/cosf/sinf/expf, the libm that a
+ * Linux build of the reference links for f32::powf/cos/sin/exp.
+ */
+#include "bnr_oracle.h"
+
+#include <immintrin.h>
+#include <math.h>
+#include <omp.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* Errors (bitnet-core/src/error.rs:12-55 Display strings)                  */
+/* ------------------------------------------------------------------------ */
+
+static __thread char g_err[512];
+
+const char *bnro_last_error(void) { return g_err; }
+
+static int fail_shape(const char *fmt_expected, const char *got) {
+  snprintf(g_err, sizeof g_err, "invalid tensor shape: expected %s, got %s",
+           fmt_expected, got);
+  return BNRO_INVALID_SHAPE;
+}
+
+static int fail_config(const char *fmt, ...) {
+  char msg[400];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(msg, sizeof msg, fmt, ap);
+  va_end(ap);
+  snprintf(g_err, sizeof g_err, "invalid model configuration: %s", msg);
+  return BNRO_INVALID_CONFIG;
+}
+
+static int ok(void) {
+  g_err[0] = 0;
+  return BNRO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Seeded generator                                                          */
+/* ------------------------------------------------------------------------ */
+
+static uint64_t splitmix64(uint64_t *state) {
+  uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+void bnro_fill_normal(uint64_t seed, float *out, size_t n, float scale) {
+  uint64_t st = seed;
+  for (size_t i = 0; i < n; i += 2) {
+    /* u1 in (0,1], u2 in [0,1) from the top 53 bits. */
+    double u1 = ((double)(splitmix64(&st) >> 11) + 1.0) * 0x1.0p-53;
+    double u2 = (double)(splitmix64(&st) >> 11) * 0x1.0p-53;
+    double r = sqrt(-2.0 * log(u1));
+    double a = 6.283185307179586476925286766559 * u2;
+    out[i] = (float)(r * cos(a)) * scale;
+    if (i + 1 < n) out[i + 1] = (float)(r * sin(a)) * scale;
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* dot / axpy / softmax                                                      */
+/* ------------------------------------------------------------------------ */
+
+static int g_force_scalar = 0;
+void bnro_force_scalar(int on) { g_force_scalar = on; }
+
+static int use_avx2_fma(void) {
+  static int cached = -1;
+  if (cached < 0) {
+    __builtin_cpu_init();
+    cached = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+  }
+  return cached && !g_force_scalar;
+}
+
+/* hsum_f32_avx2, simd.rs:292-307: ((l0+h0)+(l1+h1)) + ((l2+h2)+(l3+h3)). */
+static inline float hsum8(__m256 v) {
+  __m128 hi = _mm256_extractf128_ps(v, 1);
+  __m128 lo = _mm256_castps256_ps128(v);
+  __m128 s4 = _mm_add_ps(lo, hi);
+  __m128 sh = _mm_movehdup_ps(s4);
+  __m128 s2 = _mm_add_ps(s4, sh);
+  __m128 sh2 = _mm_movehl_ps(s2, s2);
+  __m128 s1 = _mm_add_ss(s2, sh2);
+  return _mm_cvtss_f32(s1);
+}
+
+/* dot_f32_f32_avx2, simd.rs:676-704. */
+static float dot_avx2(const float *a, const float *b, size_t n) {
+  size_t chunks = n / 8, rem = n % 8;
+  __m256 acc = _mm256_setzero_ps();
+  for (size_t i = 0; i < chunks; i++) {
+    __m256 va = _mm256_loadu_ps(a + i * 8);
+    __m256 vb = _mm256_loadu_ps(b + i * 8);
+    acc = _mm256_fmadd_ps(va, vb, acc);
+  }
+  float r = hsum8(acc);
+  size_t base = chunks * 8;
+  for (size_t i = 0; i < rem; i++) r += a[base + i] * b[base + i];
+  return r;
+}
+
+/* dot_f32_f32_scalar, simd.rs:724-731. */
+static float dot_scalar(const float *a, const float *b, size_t n) {
+  float acc = 0.0f;
+  for (size_t i = 0; i < n; i++) acc += a[i] * b[i];
+  return acc;
+}
+
+float bnro_dot_f32(const float *a, const float *b, size_t n) {
+  return use_avx2_fma() ? dot_avx2(a, b, n) : dot_scalar(a, b, n);
+}
+
+/* axpy_f32_avx2, simd.rs:743-766 (FMA body, unfused remainder). */
+static void axpy_avx2(float alpha, const float *x, float *out, size_t n) {
+  size_t chunks = n / 8, rem = n % 8;
+  __m256 va = _mm256_set1_ps(alpha);
+  for (size_t i = 0; i < chunks; i++) {
+    __m256 vx = _mm256_loadu_ps(x + i * 8);
+    __m256 vo = _mm256_loadu_ps(out + i * 8);
+    _mm256_storeu_ps(out + i * 8, _mm256_fmadd_ps(va, vx, vo));
+  }
+  size_t base = chunks * 8;
+  for (size_t i = 0; i < rem; i++) out[base + i] += alpha * x[base + i];
+}
+
+/* axpy_f32_scalar, simd.rs:786-791 (unfused). */
+static void axpy_scalar(float alpha, const float *x, float *out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] += alpha * x[i];
+}
+
+void bnro_axpy_f32(float alpha, const float *x, float *out, size_t n) {
+  if (use_avx2_fma())
+    axpy_avx2(alpha, x, out, n);
+  else
+    axpy_scalar(alpha, x, out, n);
+}
+
+/* softmax_f32, ops.rs:206-226.  f32::max ignores a NaN operand, as fmaxf. */
+void bnro_softmax_f32(float *x, size_t n) {
+  if (n == 0) return;
+  float mx = -INFINITY;
+  for (size_t i = 0; i < n; i++) mx = fmaxf(mx, x[i]);
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    x[i] = expf(x[i] - mx);
+    sum += x[i];
+  }
+  float inv = 1.0f / sum;
+  for (size_t i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* ------------------------------------------------------------------------ */
+/* RoPE                                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* Angle formula shared by RopeCache::new (rope.rs:136-145) and
+ * compute_cos_sin (rope.rs:368-382): exponent = (-2*i)/d in f32, evaluated
+ * left to right; freq = theta.powf(exponent); angle = pos as f32 * freq. */
+static inline void rope_angle(size_t pos, size_t i, size_t head_dim, float theta,
+                              float *c, float *s) {
+  float exponent = -2.0f * (float)i / (float)head_dim;
+  float freq = powf(theta, exponent);
+  float angle = (float)pos * freq;
+  *c = cosf(angle);
+  *s = sinf(angle);
+}
+
+/* RopeCache::new validation and tables, rope.rs:100-153. */
+int bnro_rope_table(size_t max_seq, size_t head_dim, float theta, float *cos_out,
+                    float *sin_out) {
+  if (head_dim == 0 || head_dim % 2 != 0)
+    return fail_config("head_dim must be even and > 0, got %zu", head_dim);
+  if (!(theta > 0.0f) || !isfinite(theta))
+    return fail_config("theta must be finite and > 0, got %g", (double)theta);
+  size_t half = head_dim / 2;
+  for (size_t pos = 0; pos < max_seq; pos++)
+    for (size_t i = 0; i < half; i++)
+      rope_angle(pos, i, head_dim, theta, &cos_out[pos * half + i],
+                 &sin_out[pos * half + i]);
+  return ok();
+}
+
+/* apply_rope_to_head_slice, rope.rs:414-430: half-split pairing (i, i+half),
+ * two products and one add/sub per output, unfused. */
+static void rope_head(float *x, const float *c, const float *s, size_t half) {
+  for (size_t i = 0; i < half; i++) {
+    float lo = x[i], hi = x[i + half];
+    x[i] = lo * c[i] - hi * s[i];
+    x[i + half] = hi * c[i] + lo * s[i];
+  }
+}
+
+static int check_qk_len(size_t q_len, size_t k_len, size_t n_heads, size_t n_kv,
+                        size_t head_dim) {
+  char e[128], g[64];
+  if (q_len != n_heads * head_dim) {
+    snprintf(e, sizeof e, "q.len() == %zu * %zu = %zu", n_heads, head_dim,
+             n_heads * head_dim);
+    snprintf(g, sizeof g, "q.len() = %zu", q_len);
+    return fail_shape(e, g);
+  }
+  if (k_len != n_kv * head_dim) {
+    snprintf(e, sizeof e, "k.len() == %zu * %zu = %zu", n_kv, head_dim,
+             n_kv * head_dim);
+    snprintf(g, sizeof g, "k.len() = %zu", k_len);
+    return fail_shape(e, g);
+  }
+  return BNRO_OK;
+}
+
+/* apply_rope, rope.rs:227-292. */
+int bnro_apply_rope(float *q, size_t q_len, float *k, size_t k_len, size_t position,
+                    size_t head_dim, size_t n_heads, size_t n_kv_heads, float theta) {
+  char g[64];
+  if (head_dim == 0 || head_dim % 2 != 0) {
+    snprintf(g, sizeof g, "head_dim = %zu", head_dim);
+    return fail_shape("head_dim must be even and > 0", g);
+  }
+  if (!(theta > 0.0f) || !isfinite(theta))
+    return fail_config("theta must be finite and > 0, got %g", (double)theta);
+  int st = check_qk_len(q_len, k_len, n_heads, n_kv_heads, head_dim);
+  if (st) return st;
+  size_t half = head_dim / 2;
+  float *c = malloc(half * sizeof(float)), *s = malloc(half * sizeof(float));
+  for (size_t i = 0; i < half; i++) rope_angle(position, i, head_dim, theta, &c[i], &s[i]);
+  for (size_t h = 0; h < n_heads; h++) rope_head(q + h * head_dim, c, s, half);
+  for (size_t h = 0; h < n_kv_heads; h++) rope_head(k + h * head_dim, c, s, half);
+  free(c);
+  free(s);
+  return ok();
+}
+
+/* apply_rope_cached, rope.rs:312-355 (+ RopeCache::at, rope.rs:165-178). */
+int bnro_apply_rope_cached(float *q, size_t q_len, float *k, size_t k_len,
+                           size_t position, size_t n_heads, size_t n_kv_heads,
+                           const float *cos_tab, const float *sin_tab, size_t max_seq,
+                           size_t head_dim) {
+  int st = check_qk_len(q_len, k_len, n_heads, n_kv_heads, head_dim);
+  if (st) return st;
+  if (position >= max_seq) {
+    char e[64], g[64];
+    snprintf(e, sizeof e, "pos < max_seq = %zu", max_seq);
+    snprintf(g, sizeof g, "pos = %zu", position);
+    return fail_shape(e, g);
+  }
+  size_t half = head_dim / 2;
+  const float *c = cos_tab + position * half, *s = sin_tab + position * half;
+  for (size_t h = 0; h < n_heads; h++) rope_head(q + h * head_dim, c, s, half);
+  for (size_t h = 0; h < n_kv_heads; h++) rope_head(k + h * head_dim, c, s, half);
+  return ok();
+}
+
+/* ------------------------------------------------------------------------ */
+/* Attention                                                                 */
+/* ------------------------------------------------------------------------ */
+
+static int g_threads = 0;
+void bnro_set_threads(int n) { g_threads = n; }
+int bnro_get_threads(void) { return g_threads > 0 ? g_threads : omp_get_num_procs(); }
+
+/* masked_attention, attention.rs:97-209: validation order 109-161, scale
+ * (sqrt(d) as f32).recip() 165, per q head: scores via dot*scale 185-189,
+ * softmax 192, zeroed output then axpy over t 195-204. */
+int bnro_masked_attention(const float *q, size_t q_len, const float *k_cache,
+                          size_t k_len, const float *v_cache, size_t v_len,
+                          float *output, size_t out_len, size_t n_heads,
+                          size_t n_kv_heads, size_t head_dim, size_t cur_pos) {
+  char e[160], g[96];
+  if (head_dim == 0) return fail_shape("head_dim > 0", "head_dim = 0");
+  if (n_kv_heads == 0) return fail_config("n_kv_heads must be > 0");
+  if (n_heads == 0) return fail_config("n_heads must be > 0");
+  if (n_heads % n_kv_heads != 0)
+    return fail_config("n_heads (%zu) must be divisible by n_kv_heads (%zu)", n_heads,
+                       n_kv_heads);
+  size_t seq_len = cur_pos + 1;
+  size_t head_stride = k_len / n_kv_heads;
+  size_t required = n_kv_heads * head_stride;
+  size_t q_expected = n_heads * head_dim;
+  if (q_len != q_expected) {
+    snprintf(e, sizeof e, "q.len() == n_heads * head_dim = %zu * %zu = %zu", n_heads,
+             head_dim, q_expected);
+    snprintf(g, sizeof g, "q.len() = %zu", q_len);
+    return fail_shape(e, g);
+  }
+  if (k_len < required) {
+    snprintf(e, sizeof e, "k_cache.len() >= %zu", required);
+    snprintf(g, sizeof g, "k_cache.len() = %zu", k_len);
+    return fail_shape(e, g);
+  }
+  if (v_len < required) {
+    snprintf(e, sizeof e, "v_cache.len() >= %zu", required);
+    snprintf(g, sizeof g, "v_cache.len() = %zu", v_len);
+    return fail_shape(e, g);
+  }
+  if (head_stride < seq_len * head_dim) {
+    snprintf(e, sizeof e, "per-head cache stride >= %zu", seq_len * head_dim);
+    snprintf(g, sizeof g, "per-head cache stride = %zu", head_stride);
+    return fail_shape(e, g);
+  }
+  if (out_len != q_expected) {
+    snprintf(e, sizeof e, "output.len() == n_heads * head_dim = %zu", q_expected);
+    snprintf(g, sizeof g, "output.len() = %zu", out_len);
+    return fail_shape(e, g);
+  }
+
+  float scale = 1.0f / sqrtf((float)head_dim);
+  size_t group = n_heads / n_kv_heads;
+  int nthr = bnro_get_threads();
+  if ((size_t)nthr > n_heads) nthr = (int)n_heads;
+
+#pragma omp parallel num_threads(nthr)
+  {
+    float *scores = malloc(seq_len * sizeof(float));
+#pragma omp for schedule(static)
+    for (long hh = 0; hh < (long)n_heads; hh++) {
+      size_t h = (size_t)hh;
+      size_t kv = h / group;
+      const float *qh = q + h * head_dim;
+      float *oh = output + h * head_dim;
+      const float *kb = k_cache + kv * head_stride;
+      const float *vb = v_cache + kv * head_stride;
+      for (size_t t = 0; t < seq_len; t++)
+        scores[t] = bnro_dot_f32(qh, kb + t * head_dim, head_dim) * scale;
+      bnro_softmax_f32(scores, seq_len);
+      for (size_t d = 0; d < head_dim; d++) oh[d] = 0.0f;
+      for (size_t t = 0; t < seq_len; t++)
+        bnro_axpy_f32(scores[t], vb + t * head_dim, oh, head_dim);
+    }
+    free(scores);
+  }
+  return ok();
+}
+
+/* ------------------------------------------------------------------------ */
+/* CpuBackend (lazy RoPE table policy)                                       */
+/* ------------------------------------------------------------------------ */
+
+struct bnro_backend {
+  int has_table;
+  size_t max_seq, head_dim;
+  float theta;
+  float *cos_tab, *sin_tab;
+};
+
+bnro_backend *bnro_backend_new(void) { return calloc(1, sizeof(bnro_backend)); }
+
+void bnro_backend_free(bnro_backend *b) {
+  if (!b) return;
+  free(b->cos_tab);
+  free(b->sin_tab);
+  free(b);
+}
+
+/* CpuBackend::rope_embed, bitnet-cpu/src/lib.rs:289-314: rebuild the table
+ * when absent, when head_dim changes, when |theta - cached| > 1e-3 or when
+ * position >= max_seq; the new max_seq is max(position + 1, 4096).  A failed
+ * rebuild leaves the previous table in place (the `?` returns before the
+ * assignment). */
+int bnro_backend_rope_embed(bnro_backend *b, float *q, size_t q_len, float *k,
+                            size_t k_len, size_t position, size_t head_dim,
+                            size_t n_heads, size_t n_kv_heads, float theta) {
+  int reinit = !b->has_table || b->head_dim != head_dim ||
+               fabsf(b->theta - theta) > 1e-3f || position >= b->max_seq;
+  if (reinit) {
+    size_t max_seq = position + 1 > 4096 ? position + 1 : 4096;
+    size_t n = max_seq * (head_dim / 2);
+    float *c = NULL, *s = NULL;
+    if (head_dim != 0 && head_dim % 2 == 0) {
+      c = malloc((n ? n : 1) * sizeof(float));
+      s = malloc((n ? n : 1) * sizeof(float));
+    }
+    int st = bnro_rope_table(max_seq, head_dim, theta, c, s);
+    if (st) {
+      free(c);
+      free(s);
+      return st;
+    }
+    free(b->cos_tab);
+    free(b->sin_tab);
+    b->cos_tab = c;
+    b->sin_tab = s;
+    b->max_seq = max_seq;
+    b->head_dim = head_dim;
+    b->theta = theta;
+    b->has_table = 1;
+  }
+  return bnro_apply_rope_cached(q, q_len, k, k_len, position, n_heads, n_kv_heads,
+                                b->cos_tab, b->sin_tab, b->max_seq, b->head_dim);
+}
+
+int bnro_backend_rope_state(const bnro_backend *b, size_t *max_seq, size_t *head_dim,
+                            float *theta) {
+  if (!b->has_table) return 0;
+  *max_seq = b->max_seq;
+  *head_dim = b->head_dim;
+  *theta = b->theta;
+  return 1;
+}
+
+/* ------------------------------------------------------------------------ */
+/* KVCache                                                                   */
+/* ------------------------------------------------------------------------ */
+
+struct bnro_kv_cache {
+  size_t n_layers, n_kv, head_dim, max_seq, filled;
+  size_t *layer_len;
+  float **k, **v;
+};
+
+/* KVCache::new, bitnet-model/src/lib.rs:148-169 (zeroed backing buffers). */
+bnro_kv_cache *bnro_kv_new(size_t n_layers, size_t n_kv_heads, size_t head_dim,
+                           size_t max_seq) {
+  bnro_kv_cache *c = calloc(1, sizeof *c);
+  c->n_layers = n_layers;
+  c->n_kv = n_kv_heads;
+  c->head_dim = head_dim;
+  c->max_seq = max_seq;
+  c->layer_len = calloc(n_layers ? n_layers : 1, sizeof(size_t));
+  c->k = calloc(n_layers ? n_layers : 1, sizeof(float *));
+  c->v = calloc(n_layers ? n_layers : 1, sizeof(float *));
+  size_t cap = max_seq * n_kv_heads * head_dim;
+  for (size_t l = 0; l < n_layers; l++) {
+    c->k[l] = calloc(cap ? cap : 1, sizeof(float));
+    c->v[l] = calloc(cap ? cap : 1, sizeof(float));
+  }
+  return c;
+}
+
+void bnro_kv_free(bnro_kv_cache *c) {
+  if (!c) return;
+  for (size_t l = 0; l < c->n_layers; l++) {
+    free(c->k[l]);
+    free(c->v[l]);
+  }
+  free(c->k);
+  free(c->v);
+  free(c->layer_len);
+  free(c);
+}
+
+/* KVCache::store_kv, bitnet-model/src/lib.rs:184-236: validation order
+ * k len, v len, position < max_seq, position <= layer length; head-major
+ * destination kv_h*max_seq*d + position*d; extends the layer when
+ * position == layer length. */
+int bnro_kv_store(bnro_kv_cache *c, size_t layer, size_t position, const float *k_vec,
+                  size_t k_len, const float *v_vec, size_t v_len) {
+  char e[96], g[64];
+  size_t stride = c->n_kv * c->head_dim;
+  if (k_len != stride) {
+    snprintf(e, sizeof e, "k_vec.len() = %zu", stride);
+    snprintf(g, sizeof g, "%zu", k_len);
+    return fail_shape(e, g);
+  }
+  if (v_len != stride) {
+    snprintf(e, sizeof e, "v_vec.len() = %zu", stride);
+    snprintf(g, sizeof g, "%zu", v_len);
+    return fail_shape(e, g);
+  }
+  if (position >= c->max_seq) {
+    snprintf(e, sizeof e, "position < max_seq (%zu)", c->max_seq);
+    snprintf(g, sizeof g, "position = %zu", position);
+    return fail_shape(e, g);
+  }
+  if (position > c->layer_len[layer]) {
+    snprintf(e, sizeof e, "position <= layer_len_positions (%zu)", c->layer_len[layer]);
+    snprintf(g, sizeof g, "position = %zu", position);
+    return fail_shape(e, g);
+  }
+  for (size_t h = 0; h < c->n_kv; h++) {
+    size_t dst = h * c->max_seq * c->head_dim + position * c->head_dim;
+    memcpy(c->k[layer] + dst, k_vec + h * c->head_dim, c->head_dim * sizeof(float));
+    memcpy(c->v[layer] + dst, v_vec + h * c->head_dim, c->head_dim * sizeof(float));
+  }
+  if (position == c->layer_len[layer]) c->layer_len[layer]++;
+  return ok();
+}
+
+/* KVCache::advance, lib.rs:244-252 (the reference panics on overflow; here
+ * the overflow is reported as a backend error so a test can observe it). */
+int bnro_kv_advance(bnro_kv_cache *c) {
+  if (c->filled >= c->max_seq) {
+    snprintf(g_err, sizeof g_err,
+             "KVCache::advance overflow: filled_positions=%zu max_seq=%zu", c->filled,
+             c->max_seq);
+    return BNRO_BACKEND_ERROR;
+  }
+  c->filled++;
+  return ok();
+}
+
+/* KVCache::clear, lib.rs:285-292. */
+void bnro_kv_clear(bnro_kv_cache *c) {
+  size_t cap = c->max_seq * c->n_kv * c->head_dim;
+  for (size_t l = 0; l < c->n_layers; l++) {
+    memset(c->k[l], 0, cap * sizeof(float));
+    memset(c->v[l], 0, cap * sizeof(float));
+    c->layer_len[l] = 0;
+  }
+  c->filled = 0;
+}
+
+size_t bnro_kv_len(const bnro_kv_cache *c) { return c->filled; }
+size_t bnro_kv_layer_len(const bnro_kv_cache *c, size_t layer) {
+  return c->layer_len[layer];
+}
+float *bnro_kv_k(bnro_kv_cache *c, size_t layer) { return c->k[layer]; }
+float *bnro_kv_v(bnro_kv_cache *c, size_t layer) { return c->v[layer]; }
+size_t bnro_kv_backing_len(const bnro_kv_cache *c) {
+  return c->max_seq * c->n_kv * c->head_dim;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Per-token call sequence of one layer                                      */
+/* ------------------------------------------------------------------------ */
+
+/* BitNetModel::forward hot calls, bitnet-model/src/lib.rs:684-718:
+ * rope_embed(q_buf, k_buf, position) -> store_kv(layer, position) ->
+ * masked_attention(q_buf, k[layer], v[layer], cur_pos = position). */
+int bnro_layer_tokens(bnro_backend *b, bnro_kv_cache *c, size_t layer, float *q_raw,
+                      float *k_raw, const float *v_raw, size_t n_tokens,
+                      size_t start_pos, size_t n_heads, size_t n_kv_heads,
+                      size_t head_dim, float theta, float *out) {
+  size_t qd = n_heads * head_dim, kd = n_kv_heads * head_dim;
+  size_t backing = bnro_kv_backing_len(c);
+  for (size_t i = 0; i < n_tokens; i++) {
+    size_t pos = start_pos + i;
+    float *q = q_raw + i * qd, *k = k_raw + i * kd;
+    const float *v = v_raw + i * kd;
+    int st = bnro_backend_rope_embed(b, q, qd, k, kd, pos, head_dim, n_heads,
+                                     n_kv_heads, theta);
+    if (st) return st;
+    st = bnro_kv_store(c, layer, pos, k, kd, v, kd);
+    if (st) return st;
+    st = bnro_masked_attention(q, qd, c->k[layer], backing, c->v[layer], backing,
+                               out + i * qd, qd, n_heads, n_kv_heads, head_dim, pos);
+    if (st) return st;
+  }
+  return ok();
+}

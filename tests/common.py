@@ -1,0 +1,138 @@
+"""Shared helpers for the test suite: tolerance rule, seeded workloads, fp64
+brute force.
+
+Tolerance (fp32 I/O): per element |gpu - ref| <= ATOL + RTOL * |ref| with
+ATOL = 2e-3, RTOL = 1e-3 (allclose semantics); max-abs and max-rel are
+reported separately in the failure message.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+ATOL = 2e-3
+RTOL = 1e-3
+
+# BitNet b1.58 2B attention shape (bitnet-core/src/config.rs:161-173).
+HQ, HKV, D, THETA = 20, 5, 128, 500000.0
+
+
+def seed(cfg: int, tensor_id: int) -> int:
+    """Seed of tensor `tensor_id` of workload `cfg`: 0xB17E7000 + 16*cfg + id."""
+    return 0xB17E7000 + 16 * cfg + tensor_id
+
+
+def assert_close(got, ref, what: str = "", atol: float = ATOL, rtol: float = RTOL) -> dict:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = np.abs(got - ref)
+    max_abs = float(err.max()) if err.size else 0.0
+    rel = err / np.maximum(np.abs(ref), 1e-30)
+    max_rel = float(rel.max()) if rel.size else 0.0
+    bad = err > atol + rtol * np.abs(ref)
+    n_bad = int(bad.sum())
+    assert n_bad == 0, (f"{what}: {n_bad}/{err.size} elements outside "
+                        f"|d| <= {atol} + {rtol}|ref| (max_abs={max_abs:.3e}, "
+                        f"max_rel={max_rel:.3e})")
+    return {"max_abs": max_abs, "max_rel": max_rel}
+
+
+# ----------------------------------------------------------------------------
+# fp64 brute force (independent of the oracle's code)
+# ----------------------------------------------------------------------------
+
+def attention_f64(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, cur_pos):
+    """Scaled dot-product GQA attention over rows 0..=cur_pos in float64;
+    the caches are head-major with per-head stride len/n_kv."""
+    q = np.asarray(q, np.float64).reshape(n_heads, head_dim)
+    stride = k_cache.size // n_kv_heads
+    L = cur_pos + 1
+    K = np.stack([np.asarray(k_cache[h * stride:h * stride + L * head_dim], np.float64)
+                  .reshape(L, head_dim) for h in range(n_kv_heads)])
+    V = np.stack([np.asarray(v_cache[h * stride:h * stride + L * head_dim], np.float64)
+                  .reshape(L, head_dim) for h in range(n_kv_heads)])
+    g = n_heads // n_kv_heads
+    out = np.empty((n_heads, head_dim))
+    for h in range(n_heads):
+        s = K[h // g] @ q[h] / np.sqrt(head_dim)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ V[h // g]
+    return out.reshape(-1)
+
+
+# ----------------------------------------------------------------------------
+# Seeded workloads
+# ----------------------------------------------------------------------------
+
+def decode_workload(cfg: int, pos: int, cap: int = 4096, q_scale: float = 1.0,
+                    n_heads: int = HQ, n_kv: int = HKV, head_dim: int = D):
+    """One decode step at `pos`: cached rows 0..pos-1 ~ N(0,1) (taken as
+    already rotated), raw q ~ N(0,1)*q_scale, raw k and v ~ N(0,1).
+    Returns dict with head-major host caches [n_kv, cap, d] (rows >= pos are
+    zero)."""
+    kc = np.zeros((n_kv, cap, head_dim), np.float32)
+    vc = np.zeros_like(kc)
+    if pos:
+        kc[:, :pos] = oracle.normal(seed(cfg, 3), (n_kv, pos, head_dim))
+        vc[:, :pos] = oracle.normal(seed(cfg, 4), (n_kv, pos, head_dim))
+    return {
+        "q": oracle.normal(seed(cfg, 0), (n_heads * head_dim,), q_scale),
+        "k": oracle.normal(seed(cfg, 1), (n_kv * head_dim,)),
+        "v": oracle.normal(seed(cfg, 2), (n_kv * head_dim,)),
+        "k_cache": kc, "v_cache": vc, "pos": pos, "cap": cap,
+    }
+
+
+def oracle_decode(w, n_heads=HQ, n_kv=HKV, head_dim=D, theta=THETA):
+    """Reference call sequence for one token: rope_embed -> store_kv ->
+    masked_attention (bitnet-model/src/lib.rs:1004-1036).  Returns
+    (q_rot, k_rot, k_cache, v_cache, out) without modifying `w`."""
+    be = oracle.CpuBackend()
+    q = w["q"].copy()
+    k = w["k"].copy()
+    be.rope_embed(q, k, w["pos"], head_dim, n_heads, n_kv, theta)
+    kc = w["k_cache"].copy()
+    vc = w["v_cache"].copy()
+    kc[:, w["pos"]] = k.reshape(n_kv, head_dim)
+    vc[:, w["pos"]] = w["v"].reshape(n_kv, head_dim)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    be.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out, n_heads, n_kv, head_dim,
+                        w["pos"])
+    return q, k, kc, vc, out
+
+
+def prefill_workload(cfg: int, n_tokens: int, n_heads: int = HQ, n_kv: int = HKV,
+                     head_dim: int = D):
+    return {
+        "q": oracle.normal(seed(cfg, 0), (n_tokens, n_heads * head_dim)),
+        "k": oracle.normal(seed(cfg, 1), (n_tokens, n_kv * head_dim)),
+        "v": oracle.normal(seed(cfg, 2), (n_tokens, n_kv * head_dim)),
+    }
+
+
+def oracle_prefill(w, start_pos=0, cap=None, n_heads=HQ, n_kv=HKV, head_dim=D, theta=THETA,
+                   cache=None, layer=0, backend=None):
+    """n_tokens serial rope -> store_kv -> masked_attention calls of one layer
+    (bitnet-model/src/lib.rs:684-718).  Returns (q_rot, k_rot, KVCache, out)."""
+    n = w["q"].shape[0]
+    cap = cap or max(start_pos + n, 1)
+    if cache is None:
+        cache = oracle.KVCache(1, n_kv, head_dim, cap)
+    if backend is None:
+        backend = oracle.CpuBackend()
+    q = w["q"].copy()
+    k = w["k"].copy()
+    out = oracle.layer_tokens(backend, cache, layer, q, k, w["v"], start_pos, n_heads, n_kv,
+                              head_dim, theta)
+    return q, k, cache, out
+
+
+def batched_lengths(n: int = 32, lo: int = 128, hi: int = 4096, cfg: int = 4):
+    """Cached lengths ~ U[lo, hi) (half-open, as Rust's gen_range) from a
+    seeded PCG64 stream."""
+    rng = np.random.default_rng(seed(cfg, 15))
+    return rng.integers(lo, hi, size=n).astype(np.int32)

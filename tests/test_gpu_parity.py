@@ -1,0 +1,316 @@
+"""GPU parity of the HIP path against the oracle (the C restatement of the
+reference's CPU path), through the C ABI.
+
+Bit-exact: rotated q/k and appended cache rows.  Attention outputs: per
+element |gpu - ref| <= 2e-3 + 1e-3|ref| (fp32 I/O).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from common import (D, HKV, HQ, THETA, assert_close, batched_lengths, decode_workload,
+                    oracle_decode, oracle_prefill, prefill_workload, seed)
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+
+
+def case(msg):
+    print(f"[gpu case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+# --- trait-shaped host entry points ------------------------------------------------
+
+def test_host_closed_forms(backend):
+    case("host closed forms (attention.rs:248-719)")
+    out = np.zeros(4, f32)
+    backend.masked_attention(np.array([1, 0, 0, 0], f32), np.array([1, 0, 0, 0], f32),
+                             np.array([.1, .2, .3, .4], f32), out, 1, 1, 4, 0)
+    np.testing.assert_allclose(out, [.1, .2, .3, .4], atol=1e-5)
+    out = np.zeros(2, f32)
+    backend.masked_attention(np.zeros(2, f32), np.arange(1, 7, dtype=f32),
+                             np.array([1, 0, 2, 0, 3, 0], f32), out, 1, 1, 2, 2)
+    np.testing.assert_allclose(out, [2, 0], atol=1e-5)
+    out = np.zeros(8, f32)
+    backend.masked_attention(np.zeros(8, f32), np.zeros(4, f32), np.array([1, 0, 0, 1], f32),
+                             out, 4, 2, 2, 0)
+    np.testing.assert_allclose(out, [1, 0, 1, 0, 0, 1, 0, 1], atol=1e-5)
+    out = np.zeros(20 * 128, f32)
+    backend.masked_attention(np.zeros(20 * 128, f32), np.zeros(4 * 640, f32),
+                             np.full(4 * 640, 0.1, f32), out, 20, 5, 128, 3)
+    np.testing.assert_allclose(out, 0.1, atol=1e-5)
+
+
+@pytest.mark.parametrize("args", [
+    (7, 8, 8, 8, 2, 2, 4, 0), (8, 8, 8, 6, 2, 2, 4, 0), (8, 3, 8, 8, 2, 2, 4, 0),
+    (8, 8, 3, 8, 2, 2, 4, 0), (12, 8, 8, 12, 3, 2, 4, 0), (0, 0, 0, 0, 1, 1, 0, 0),
+    (4, 0, 0, 4, 1, 0, 4, 0), (4, 8, 8, 4, 1, 1, 4, 2),
+])
+def test_host_error_kinds_match_oracle(backend, args):
+    case(f"host error kinds {args}")
+    import bitnetrs_amd
+
+    arrs = [np.zeros(n, f32) for n in args[:4]]
+    with pytest.raises(oracle.OracleError) as e_ref:
+        oracle.masked_attention(*arrs, *args[4:])
+    with pytest.raises(bitnetrs_amd.BitNetError) as e_gpu:
+        backend.masked_attention(*arrs, *args[4:])
+    assert e_gpu.value.kind == e_ref.value.kind
+    assert str(e_gpu.value) == str(e_ref.value)
+
+
+def test_host_rope_embed_bit_exact(backend):
+    case("host rope_embed bit-exact, d=128 theta=5e5, positions 0..4100")
+    ref = oracle.CpuBackend()
+    for pos in [0, 1, 2, 511, 4095, 4100]:
+        q = oracle.normal(seed(1, 0) + pos, (HQ * D,))
+        k = oracle.normal(seed(1, 1) + pos, (HKV * D,))
+        q2, k2 = q.copy(), k.copy()
+        ref.rope_embed(q, k, pos, D, HQ, HKV, THETA)
+        backend.rope_embed(q2, k2, pos, D, HQ, HKV, THETA)
+        np.testing.assert_array_equal(q2, q)
+        np.testing.assert_array_equal(k2, k)
+
+
+def test_host_rope_embed_errors(backend):
+    case("host rope_embed errors")
+    import bitnetrs_amd
+
+    with pytest.raises(bitnetrs_amd.InvalidConfig):
+        backend.rope_embed(np.zeros(7, f32), np.zeros(7, f32), 0, 7, 1, 1, 1e4)
+    with pytest.raises(bitnetrs_amd.InvalidConfig):
+        backend.rope_embed(np.zeros(8, f32), np.zeros(8, f32), 0, 8, 1, 1, 0.0)
+    with pytest.raises(bitnetrs_amd.InvalidShape):
+        backend.rope_embed(np.zeros(7, f32), np.zeros(8, f32), 0, 8, 1, 1, 1e4)
+
+
+def test_host_decode_sequence_c1(backend):
+    case("host path C1: rope_embed -> store -> masked_attention at pos 511")
+    backend.mirror_invalidate()  # a recycled host address must not look in sync
+    w = decode_workload(1, 511)
+    q_ref, k_ref, _, _, out_ref = oracle_decode(w)
+    q, k = w["q"].copy(), w["k"].copy()
+    backend.rope_embed(q, k, 511, D, HQ, HKV, THETA)
+    np.testing.assert_array_equal(q, q_ref)
+    np.testing.assert_array_equal(k, k_ref)
+    kc, vc = w["k_cache"].copy(), w["v_cache"].copy()
+    kc[:, 511] = k.reshape(HKV, D)
+    vc[:, 511] = w["v"].reshape(HKV, D)
+    out = np.zeros(HQ * D, f32)
+    backend.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out, HQ, HKV, D, 511)
+    print(assert_close(out, out_ref, "C1 host"))
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(20, 5, 128), (8, 8, 128), (8, 4, 128),
+                                            (4, 2, 16), (6, 3, 64), (8, 1, 128)])
+def test_host_mirror_incremental_decode(backend, n_heads, n_kv, hd):
+    case(f"host mirror: 40 decode steps + rewind, heads {n_heads}/{n_kv} d {hd}")
+    cap = 64
+    ref = oracle.CpuBackend()
+    kc = np.zeros((n_kv, cap, hd), f32)
+    vc = np.zeros_like(kc)
+    for step in range(40):
+        q = oracle.normal(seed(30, 0) + step, (n_heads * hd,))
+        k = oracle.normal(seed(30, 1) + step, (n_kv * hd,))
+        v = oracle.normal(seed(30, 2) + step, (n_kv * hd,))
+        ref.rope_embed(q, k, step, hd, n_heads, n_kv, 10000.0)
+        kc[:, step] = k.reshape(n_kv, hd)
+        vc[:, step] = v.reshape(n_kv, hd)
+        out_ref = np.zeros(n_heads * hd, f32)
+        oracle.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out_ref, n_heads, n_kv, hd,
+                                step)
+        out = np.zeros_like(out_ref)
+        backend.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out, n_heads, n_kv, hd, step)
+        assert_close(out, out_ref, f"step {step}")
+    # rewind (new conversation into the same buffers): full resync
+    kc[:] = oracle.normal(seed(30, 5), kc.shape)
+    out_ref = np.zeros(n_heads * hd, f32)
+    oracle.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out_ref, n_heads, n_kv, hd, 5)
+    out = np.zeros_like(out_ref)
+    backend.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out, n_heads, n_kv, hd, 5)
+    assert_close(out, out_ref, "rewind")
+
+
+def test_host_mirror_invalidate_and_full_mode(backend):
+    case("host mirror invalidate / full mode")
+    import bitnetrs_amd
+
+    backend.mirror_invalidate()
+    w = decode_workload(31, 100, cap=128)
+    kc, vc = w["k_cache"].reshape(-1), w["v_cache"].reshape(-1)
+    q = w["q"]
+    out = np.zeros(HQ * D, f32)
+    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 99)
+    kc[5 * D:6 * D] += 3.0  # rewrite an old row of kv head 0
+    ref = np.zeros_like(out)
+    oracle.masked_attention(q, kc, vc, ref, HQ, HKV, D, 100)
+    backend.mirror_invalidate()
+    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 100)
+    assert_close(out, ref, "after invalidate")
+    backend.set_mirror_mode(bitnetrs_amd.BNR_MIRROR_FULL)
+    try:
+        vc[7 * D:8 * D] -= 2.0
+        oracle.masked_attention(q, kc, vc, ref, HQ, HKV, D, 101)
+        backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 101)
+        assert_close(out, ref, "full mode")
+    finally:
+        backend.set_mirror_mode(bitnetrs_amd.BNR_MIRROR_INCREMENTAL)
+
+
+# --- device entry points -----------------------------------------------------------
+
+@pytest.mark.parametrize("cfg,pos,q_scale", [(1, 511, 1.0), (2, 4095, 4.0), (5, 0, 1.0),
+                                             (6, 1, 1.0), (7, 16, 1.0), (8, 1000, 2.0),
+                                             (9, 2047, 1.0)])
+def test_dev_decode_step_fused(backend, cfg, pos, q_scale):
+    case(f"fused decode step cfg {cfg} pos {pos} q*{q_scale}")
+    import torch
+
+    w = decode_workload(cfg, pos, cap=4096, q_scale=q_scale)
+    q_ref, k_ref, kc_ref, vc_ref, out_ref = oracle_decode(w)
+    q, k, v = dev(w["q"]), dev(w["k"]), dev(w["v"])
+    kc, vc = dev(w["k_cache"]), dev(w["v_cache"])
+    out = torch.zeros(HQ * D, device="cuda")
+    q_rot = torch.zeros_like(q)
+    k_rot = torch.zeros_like(k)
+    backend.dev_decode_step(q, k, v, pos, HQ, HKV, D, THETA, kc, vc, 4096, out, q_rot, k_rot)
+    np.testing.assert_array_equal(host(q_rot), q_ref)
+    np.testing.assert_array_equal(host(k_rot), k_ref)
+    np.testing.assert_array_equal(host(kc)[:, pos], kc_ref[:, pos])
+    np.testing.assert_array_equal(host(vc)[:, pos], vc_ref[:, pos])
+    np.testing.assert_array_equal(host(q), w["q"])  # inputs untouched
+    print(assert_close(host(out), out_ref, f"decode cfg {cfg}"))
+
+
+@pytest.mark.parametrize("pos", [0, 63, 64, 511, 4095])
+def test_dev_decode_attention_prerotated(backend, pos):
+    case(f"decode attention (pre-rotated q) pos {pos}")
+    import torch
+
+    w = decode_workload(40, pos, cap=4096)
+    q_ref, _, kc_ref, vc_ref, out_ref = oracle_decode(w)
+    out = torch.zeros(HQ * D, device="cuda")
+    backend.dev_decode_attention(dev(q_ref), dev(kc_ref), dev(vc_ref), 4096, out, HQ, HKV, D, pos)
+    assert_close(host(out), out_ref, f"decode attention pos {pos}")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(4, 4, 128), (8, 4, 128), (16, 2, 64), (6, 2, 16)])
+def test_dev_decode_step_other_shapes(backend, n_heads, n_kv, hd):
+    case(f"decode step heads {n_heads}/{n_kv} d {hd}")
+    import torch
+
+    pos = 300
+    w = decode_workload(41, pos, cap=512, n_heads=n_heads, n_kv=n_kv, head_dim=hd)
+    q_ref, k_ref, kc_ref, _, out_ref = oracle_decode(w, n_heads, n_kv, hd)
+    kc, vc = dev(w["k_cache"]), dev(w["v_cache"])
+    out = torch.zeros(n_heads * hd, device="cuda")
+    k_rot = torch.zeros(n_kv * hd, device="cuda")
+    backend.dev_decode_step(dev(w["q"]), dev(w["k"]), dev(w["v"]), pos, n_heads, n_kv, hd, THETA,
+                            kc, vc, 512, out, None, k_rot)
+    np.testing.assert_array_equal(host(k_rot), k_ref)
+    np.testing.assert_array_equal(host(kc)[:, pos], kc_ref[:, pos])
+    assert_close(host(out), out_ref, "other shape")
+
+
+def test_dev_batched_decode_c4(backend):
+    case("batched decode C4: 32 seqs, lengths U[128,4096)")
+    import torch
+
+    lens = batched_lengths()
+    B, cap = len(lens), 4096
+    q = oracle.normal(seed(4, 0), (B, HQ * D))
+    k = oracle.normal(seed(4, 1), (B, HKV * D))
+    v = oracle.normal(seed(4, 2), (B, HKV * D))
+    kc = oracle.normal(seed(4, 3), (B, HKV, cap, D))
+    vc = oracle.normal(seed(4, 4), (B, HKV, cap, D))
+    d_kc, d_vc = dev(kc), dev(vc)
+    out = torch.zeros(B, HQ * D, device="cuda")
+    backend.dev_decode_step_batched(dev(q), dev(k), dev(v), lens, HQ, HKV, D, THETA, d_kc, d_vc,
+                                    cap, out)
+    got = host(out)
+    gk = host(d_kc)
+    for b in range(B):
+        w = {"q": q[b], "k": k[b], "v": v[b], "k_cache": kc[b], "v_cache": vc[b],
+             "pos": int(lens[b]), "cap": cap}
+        _, k_ref, _, _, out_ref = oracle_decode(w)
+        np.testing.assert_array_equal(gk[b][:, lens[b]], k_ref.reshape(HKV, D))
+        assert_close(got[b], out_ref, f"seq {b} len {lens[b]}")
+
+
+def test_dev_batched_decode_edge_lengths(backend):
+    case("batched decode edge lengths 0,1,15,16,17,...; batch 70 > one launch")
+    import torch
+
+    lens = np.resize(np.array([0, 1, 15, 16, 17, 31, 32, 33, 255, 256, 257, 1023], np.int32), 70)
+    B, cap = len(lens), 1024
+    q = oracle.normal(seed(42, 0), (B, HQ * D))
+    k = oracle.normal(seed(42, 1), (B, HKV * D))
+    v = oracle.normal(seed(42, 2), (B, HKV * D))
+    kc = oracle.normal(seed(42, 3), (B, HKV, cap, D))
+    vc = oracle.normal(seed(42, 4), (B, HKV, cap, D))
+    out = torch.zeros(B, HQ * D, device="cuda")
+    backend.dev_decode_step_batched(dev(q), dev(k), dev(v), lens, HQ, HKV, D, THETA, dev(kc),
+                                    dev(vc), cap, out)
+    got = host(out)
+    for b in range(B):
+        w = {"q": q[b], "k": k[b], "v": v[b], "k_cache": kc[b], "v_cache": vc[b],
+             "pos": int(lens[b]), "cap": cap}
+        assert_close(got[b], oracle_decode(w)[4], f"seq {b} len {lens[b]}")
+
+
+@pytest.mark.parametrize("n_tokens,start", [(2048, 0), (100, 0), (37, 200)])
+def test_dev_prefill(backend, n_tokens, start):
+    case(f"prefill n {n_tokens} start {start}")
+    import torch
+
+    cap = 2048 if start == 0 and n_tokens == 2048 else 512
+    w = prefill_workload(3, n_tokens)
+    cache = oracle.KVCache(1, HKV, D, cap)
+    be = oracle.CpuBackend()
+    d_kc = torch.zeros(HKV, cap, D, device="cuda")
+    d_vc = torch.zeros_like(d_kc)
+    if start:
+        pre = prefill_workload(33, start)
+        oracle_prefill(pre, cache=cache, backend=be)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(HKV, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(HKV, cap, D)))
+    q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be)
+    q, k = dev(w["q"]), dev(w["k"])
+    out = torch.zeros(n_tokens, HQ * D, device="cuda")
+    backend.dev_prefill(q, k, dev(w["v"]), n_tokens, start, HQ, HKV, D, THETA, d_kc, d_vc, cap, out)
+    np.testing.assert_array_equal(host(q), q_ref)
+    np.testing.assert_array_equal(host(k), k_ref)
+    np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+    np.testing.assert_array_equal(host(d_vc).reshape(-1), cache.v(0))
+    print(assert_close(host(out), out_ref, f"prefill {n_tokens}"))
+
+
+def test_dev_argument_errors(backend):
+    case("device entry point errors")
+    import bitnetrs_amd
+    import torch
+
+    t = torch.zeros(HQ * D, device="cuda")
+    kc = torch.zeros(HKV, 16, D, device="cuda")
+    with pytest.raises(bitnetrs_amd.InvalidShape):  # position >= cap
+        backend.dev_decode_step(t, t[:HKV * D], t[:HKV * D], 16, HQ, HKV, D, THETA, kc, kc, 16, t)
+    with pytest.raises(bitnetrs_amd.InvalidConfig):
+        backend.dev_decode_attention(t, kc, kc, 16, t, 20, 3, D, 0)
+    with pytest.raises(bitnetrs_amd.InvalidConfig):
+        backend.dev_rope_append(t, t, t, 1, 0, HQ, HKV, D, -1.0, kc, kc, 16)
