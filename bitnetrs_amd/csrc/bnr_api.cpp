@@ -131,6 +131,7 @@ struct bnr_ctx {
   // decode planner
   int target_wgs = 640;
   int force_rpg = 0;
+  int merge_inline = 1;
 };
 
 namespace {
@@ -289,11 +290,12 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
   plan_decode(c, lens, batch, n_kv, a);
   a.n_kv = n_kv;
   a.group = group;
+  a.merge_inline = c->merge_inline;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
   const size_t splits = (size_t)a.split_off[batch];
   int st = ensure_ws(c, splits * n_kv * group * kHeadDim, splits * n_kv * group);
   if (st) return st;
-  st = ensure_counters(c, (size_t)batch * n_kv);
+  st = ensure_counters(c, (size_t)batch * n_kv * kCounterStride);
   if (st) return st;
   a.ws_o = c->ws_o;
   a.ws_ml = c->ws_ml;
@@ -375,6 +377,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     return err_hip(e, "hipStreamCreate");
   }
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
+  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_inline = atoi(v) != 0;
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
     if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;

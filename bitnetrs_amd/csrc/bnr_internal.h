@@ -16,6 +16,8 @@ constexpr int kMaxBatchPerLaunch = 64;
 // Upper bound on context splits per (sequence, kv head); longer contexts
 // give each workgroup several passes over its rows.
 constexpr int kMaxSplits = 256;
+// Ticket counters are 256 bytes apart: atomics on one cache line serialise.
+constexpr int kCounterStride = 64;
 
 // RoPE + append over n_tokens consecutive positions of one sequence.  q and
 // k are rotated in place; when k_cache is non-null the rotated k rows and the
@@ -46,12 +48,13 @@ struct DecodeArgs {
   const float *cos_tab, *sin_tab; // [table_len x 64] or null (q pre-rotated)
   float *ws_o;                    // split partials: [split][n_kv][G][128]
   float2 *ws_ml;                  // split (max, sum): [split][n_kv][G]
-  unsigned *counters;             // [batch][n_kv], zero between launches
+  unsigned *counters;             // [batch][n_kv] x kCounterStride, zero between launches
   float scale_log2;               // log2(e) / sqrt(128)
   int n_kv, group, batch;
   int rows_per_split;             // rows a workgroup owns (16*RPG*passes)
   int rpg;                        // rows per 16-lane row group and pass
   int passes;
+  int merge_inline;                // 1: last-workgroup merge; 0: second kernel
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
 };

@@ -94,6 +94,31 @@ __device__ __forceinline__ float row_sum16(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max / sum over the 16 lanes of a DPP row (every lane of the row gets it).
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return v;
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Wave-uniform max / sum over 64 lanes: DPP inside each row, then the four
+// row results through readlane.
+__device__ __forceinline__ float wave_max(float v) {
+  v = row_max16(v);
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
 __device__ __forceinline__ float dot8(float4 alo, float4 ahi, float4 blo, float4 bhi) {
   float d = alo.x * blo.x;
   d = fmaf(alo.y, blo.y, d);
@@ -123,6 +148,111 @@ __device__ __forceinline__ void st4(float *p, float4 v) {
   *reinterpret_cast<float4 *>(p) = v;
 }
 
+// Agent-coherent scalar store / load: performed at the device-wide coherence
+// point, so another workgroup -- on any XCD, behind its own L2 -- that reads
+// after observing the ticket below sees the value without a cache writeback
+// or invalidate of the whole L2.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the nsplit partial states of (sequence b, kv head h) into the
+// output.  CH splits per round: one load round trip, then wave w computes
+// the round's max and split weights of q head g = w, w+4, ... (one lane per
+// split, wave reductions), and every lane forms its outputs as an
+// independent weighted sum.  AGENT: the partials were written by other
+// workgroups of this launch (agent-coherent loads); otherwise by an earlier
+// kernel (plain loads).  lds: at least 64*G + 3*G floats.
+template <int G, bool AGENT>
+__device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, int nsplit,
+                                             float *lds) {
+  constexpr int D = kHeadDim;
+  constexpr int EPT = (G * D + 255) / 256;  // output elements per lane
+  constexpr int CH = 64 / EPT;              // splits per round (at most one per lane)
+  constexpr int GPW = (G + 3) / 4;          // q heads per wave
+  float *s_w = lds;             // [G][CH] split weights of the round
+  float *s_M = s_w + CH * G;    // [G] running max
+  float *s_L = s_M + G;         // [G] running sum
+  float *s_sc = s_L + G;        // [G] rescale of the earlier rounds
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int gs0 = a.split_off[b];
+  const long long step = (long long)a.n_kv * G * D;
+  const float *po = a.ws_o + ((long long)gs0 * a.n_kv + h) * G * D;
+  if (tid < G) {
+    s_M[tid] = -INFINITY;
+    s_L[tid] = 0.f;
+  }
+  // Lane element k: e = tid + 256k (G == 1: lanes 128..255 shadow 0..127).
+  int ek[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) ek[k] = (tid + 256 * k) % (G * D);
+  float Or[EPT];
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) Or[k] = 0.f;
+  for (int c0 = 0; c0 < nsplit; c0 += CH) {
+    const int n = min(CH, nsplit - c0);
+    // One batch of loads; split indices past the end are clamped (their
+    // weight is zero), so there are no branches between loads.
+    float ov[EPT][CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const float *pu = po + (long long)min(c0 + u, nsplit - 1) * step;
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) ov[k][u] = AGENT ? ld_agent(pu + ek[k]) : pu[ek[k]];
+    }
+    float2 mlr[GPW];
+#pragma unroll
+    for (int r = 0; r < GPW; ++r) {
+      const int g = min(wv + 4 * r, G - 1);
+      const float *ml = reinterpret_cast<const float *>(
+          &a.ws_ml[((long long)(gs0 + min(c0 + lane, nsplit - 1)) * a.n_kv + h) * G + g]);
+      mlr[r] = AGENT ? make_float2(ld_agent(ml), ld_agent(ml + 1)) : make_float2(ml[0], ml[1]);
+    }
+    __syncthreads();  // earlier round's readers of s_w / s_sc are done
+#pragma unroll
+    for (int r = 0; r < GPW; ++r) {
+      const int g = wv + 4 * r;
+      if (g >= G) continue;
+      const float m = lane < n ? mlr[r].x : -INFINITY;
+      const float m_old = s_M[g];
+      const float mn = fmaxf(m_old, wave_max(m));
+      const float w = lane < n ? fast_exp2(m - mn) : 0.f;
+      const float ls = wave_sum(w * mlr[r].y);
+      if (lane < CH) s_w[g * CH + lane] = w;
+      if (lane == 0) {
+        const float sc = fast_exp2(m_old - mn);  // 0 on the first round
+        s_sc[g] = sc;
+        s_L[g] = fmaf(s_L[g], sc, ls);
+        s_M[g] = mn;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int g = ek[k] / D;
+      const float4 *w4 = reinterpret_cast<const float4 *>(s_w + g * CH);
+      float o = Or[k] * s_sc[g];
+#pragma unroll
+      for (int u4 = 0; u4 < CH / 4; ++u4) {
+        const float4 w = w4[u4];
+        o = fmaf(w.x, ov[k][4 * u4 + 0], o);
+        o = fmaf(w.y, ov[k][4 * u4 + 1], o);
+        o = fmaf(w.z, ov[k][4 * u4 + 2], o);
+        o = fmaf(w.w, ov[k][4 * u4 + 3], o);
+      }
+      Or[k] = o;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < EPT; ++k) {
+    if (tid + 256 * k < G * D)
+      a.out[b * a.out_bstride + (long long)h * G * D + ek[k]] = Or[k] / s_L[ek[k] / D];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Split-K decode attention, head_dim 128.
 //
@@ -131,20 +261,25 @@ __device__ __forceinline__ void st4(float *p, float4 v) {
 // half, so one instruction of a wave reads four 256-byte row halves, and the
 // half-split RoPE pair (i, i+64) of a q/k element sits in the same lane.
 //
-// Row r of pass p, iteration i of row group rg is t0 + p*16*RPG + i*16 + rg.
-// Each row group keeps an online-softmax state (m, l, o[G][8 dims per lane]);
-// the 16 states are merged through LDS into one (m, l, o) per workgroup,
-// written to the split workspace, and the last workgroup of a
-// (sequence, kv head) to arrive -- found with an agent-scope ticket -- merges
-// all splits and writes the output.  The ticket counter is reset by that
-// workgroup, so no memset is needed between launches.
+// Row of pass p, iteration i of row group rg: t0 + p*16*RPG + i*16 + rg.
+// The first pass's K/V loads are issued before anything else so that the
+// kernel pays one memory round trip, not a q round trip followed by a K/V
+// one.  Each row group keeps an online-softmax state (m, l, o[G][8 dims per
+// lane]); the 16 states merge through LDS into one (m, l, o) per workgroup.
+//
+// With several splits per (sequence, kv head), each workgroup stores its
+// state with agent-coherent stores, waits for them to complete and takes a
+// ticket with a relaxed agent-scope atomic; the workgroup that draws the last
+// ticket merges all splits (agent-coherent loads, one round trip per 64
+// splits) and writes the output.  It also resets the ticket counter, so no
+// memset is needed between launches.
 // ---------------------------------------------------------------------------
-template <int G, int RPG>
+template <int G, int RPG, bool INLINE>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   __shared__ float s_o[16][G][D];
-  __shared__ float s_m[16][G];
-  __shared__ float s_l[16][G];
+  __shared__ float s_m[G][16];
+  __shared__ float s_l[G][16];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -164,9 +299,10 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
 
   float *kc = a.k_cache + b * a.cache_bstride + h * a.kv_stride;
   float *vc = a.v_cache + b * a.cache_bstride + h * a.kv_stride;
-  const float *qb = a.q + b * a.q_bstride + (long long)h * G * D;
 
-  // ---- q for the G heads of this kv head (rotated here when fused) ----
+  // ---- loads of the first pass, in use order: q (+cos/sin), K rows, V rows.
+  // One batch, one memory round trip; rows are consumed as they arrive.
+  const float *qb = a.q + b * a.q_bstride + (long long)h * G * D;
   float4 qlo[G], qhi[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -178,6 +314,29 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   if (rope) {
     cs = ld4(a.cos_tab + (long long)pos * 64 + 4 * j);
     sn = ld4(a.sin_tab + (long long)pos * 64 + 4 * j);
+  }
+  float4 klo[RPG], khi[RPG], vlo[RPG], vhi[RPG];
+  bool valid[RPG];
+  auto load_pass = [&](int tp) {
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const int t = tp + i * 16 + rg;
+      valid[i] = t < t1;
+      const long long off = (long long)(valid[i] ? t : t0) * D;
+      klo[i] = ld4(kc + off + 4 * j);
+      khi[i] = ld4(kc + off + 64 + 4 * j);
+    }
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const long long off = (long long)(valid[i] ? tp + i * 16 + rg : t0) * D;
+      vlo[i] = ld4(vc + off + 4 * j);
+      vhi[i] = ld4(vc + off + 64 + 4 * j);
+    }
+  };
+  load_pass(t0);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the math
+
+  if (rope) {
 #pragma unroll
     for (int g = 0; g < G; ++g) rot4(qlo[g], qhi[g], cs, sn, qlo[g], qhi[g]);
   }
@@ -226,18 +385,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   for (int p = 0; p < a.passes; ++p) {
     const int tp = t0 + p * 16 * RPG;
     if (tp >= t1) break;
-    float4 klo[RPG], khi[RPG], vlo[RPG], vhi[RPG];
-    bool valid[RPG];
-#pragma unroll
-    for (int i = 0; i < RPG; ++i) {
-      const int t = tp + i * 16 + rg;
-      valid[i] = t < t1;
-      const long long off = (long long)(valid[i] ? t : t0) * D;
-      klo[i] = ld4(kc + off + 4 * j);
-      khi[i] = ld4(kc + off + 64 + 4 * j);
-      vlo[i] = ld4(vc + off + 4 * j);
-      vhi[i] = ld4(vc + off + 64 + 4 * j);
-    }
+    if (p > 0) load_pass(tp);
     if (own_pos) {
 #pragma unroll
       for (int i = 0; i < RPG; ++i) {
@@ -292,8 +440,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     st4(&s_o[rg][g][4 * j], olo[g]);
     st4(&s_o[rg][g][64 + 4 * j], ohi[g]);
     if (j == 0) {
-      s_m[rg][g] = m_run[g];
-      s_l[rg][g] = l_run[g];
+      s_m[g][rg] = m_run[g];
+      s_l[g][rg] = l_run[g];
     }
   }
   __syncthreads();
@@ -301,75 +449,67 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   const int gs = a.split_off[b] + s;  // global split index
   for (int e = tid; e < G * D; e += 256) {
     const int g = e / D, dim = e % D;
-    float M = -INFINITY;
+    float mr[16], lr[16], orr[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) M = fmaxf(M, s_m[r][g]);
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const float4 m4 = *reinterpret_cast<const float4 *>(&s_m[g][4 * r4]);
+      const float4 l4 = *reinterpret_cast<const float4 *>(&s_l[g][4 * r4]);
+      mr[4 * r4] = m4.x, mr[4 * r4 + 1] = m4.y, mr[4 * r4 + 2] = m4.z, mr[4 * r4 + 3] = m4.w;
+      lr[4 * r4] = l4.x, lr[4 * r4 + 1] = l4.y, lr[4 * r4 + 2] = l4.z, lr[4 * r4 + 3] = l4.w;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) orr[r] = s_o[r][g][dim];
+    float M = mr[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) M = fmaxf(M, mr[r]);
     float Ls = 0.f, O = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float w = fast_exp2(s_m[r][g] - M);  // 0 for an empty row group
-      Ls = fmaf(s_l[r][g], w, Ls);
-      O = fmaf(s_o[r][g][dim], w, O);
+      const float w = fast_exp2(mr[r] - M);  // 0 for an empty row group
+      Ls = fmaf(lr[r], w, Ls);
+      O = fmaf(orr[r], w, O);
     }
     if (nsplit == 1) {
       a.out[b * a.out_bstride + ((long long)h * G + g) * D + dim] = O / Ls;
+    } else if (INLINE) {
+      st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], O);
+      if (dim == 0) {
+        float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + g]);
+        st_agent(ml, M);
+        st_agent(ml + 1, Ls);
+      }
     } else {
-      a.ws_o[(((long long)gs * a.n_kv + h) * G + g) * D + dim] = O;
+      a.ws_o[((long long)gs * a.n_kv + h) * G * D + e] = O;
       if (dim == 0) a.ws_ml[((long long)gs * a.n_kv + h) * G + g] = make_float2(M, Ls);
     }
   }
-  if (nsplit == 1) return;
+  if (nsplit == 1 || !INLINE) return;
 
-  // ---- last workgroup of this (sequence, kv head) merges the splits ----
-  __threadfence();
+  // ---- ticket: the last workgroup of this (sequence, kv head) merges ----
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
   __syncthreads();
-  unsigned *ctr = a.counters + b * a.n_kv + h;
+  unsigned *ctr = a.counters + (b * a.n_kv + h) * kCounterStride;
   if (tid == 0) {
     const unsigned ticket =
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (ticket == (unsigned)(nsplit - 1));
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // (max, sum) of every split of this kv head into LDS (reusing s_o).
-  float2 *s_ml = reinterpret_cast<float2 *>(&s_o[0][0][0]);
-  const int gs0 = a.split_off[b];
-  for (int idx = tid; idx < nsplit * G; idx += 256) {
-    const int sp = idx / G, g = idx % G;
-    s_ml[idx] = a.ws_ml[((long long)(gs0 + sp) * a.n_kv + h) * G + g];
-  }
-  __syncthreads();
-  for (int e = tid; e < G * D; e += 256) {
-    const int g = e / D, dim = e % D;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, s_ml[sp * G + g].x);
-    float Ls = 0.f, O = 0.f;
-    const float *po = a.ws_o + (((long long)gs0 * a.n_kv + h) * G + g) * D + dim;
-    const long long step = (long long)a.n_kv * G * D;
-    int sp = 0;
-    for (; sp + 8 <= nsplit; sp += 8) {
-      float ov[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) ov[u] = po[(sp + u) * step];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float2 ml = s_ml[(sp + u) * G + g];
-        const float w = fast_exp2(ml.x - M);
-        Ls = fmaf(ml.y, w, Ls);
-        O = fmaf(ov[u], w, O);
-      }
-    }
-    for (; sp < nsplit; ++sp) {
-      const float2 ml = s_ml[sp * G + g];
-      const float w = fast_exp2(ml.x - M);
-      Ls = fmaf(ml.y, w, Ls);
-      O = fmaf(po[sp * step], w, O);
-    }
-    a.out[b * a.out_bstride + ((long long)h * G + g) * D + dim] = O / Ls;
-  }
+  merge_splits<G, true>(a, b, h, nsplit, &s_o[0][0][0]);
+}
+
+// Second kernel of the two-launch decode: one workgroup per (kv head,
+// sequence) merges the split partials written by decode_kernel<.., false>.
+template <int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+  __shared__ float lds[64 * G + 3 * G];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int nsplit = a.split_off[b + 1] - a.split_off[b];
+  if (nsplit == 1) return;
+  merge_splits<G, false>(a, b, h, nsplit, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -426,17 +566,24 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeGenericArgs a
   }
 }
 
-template <int G>
-hipError_t launch_decode_g(const DecodeArgs &a, hipStream_t s) {
+template <int G, bool INLINE>
+hipError_t launch_decode_gi(const DecodeArgs &a, hipStream_t s) {
   dim3 grid(a.split_off[a.batch], a.n_kv), block(256);
   switch (a.rpg) {
-    case 1: decode_kernel<G, 1><<<grid, block, 0, s>>>(a); break;
-    case 2: decode_kernel<G, 2><<<grid, block, 0, s>>>(a); break;
-    case 4: decode_kernel<G, 4><<<grid, block, 0, s>>>(a); break;
-    case 8: decode_kernel<G, 8><<<grid, block, 0, s>>>(a); break;
+    case 1: decode_kernel<G, 1, INLINE><<<grid, block, 0, s>>>(a); break;
+    case 2: decode_kernel<G, 2, INLINE><<<grid, block, 0, s>>>(a); break;
+    case 4: decode_kernel<G, 4, INLINE><<<grid, block, 0, s>>>(a); break;
+    case 8: decode_kernel<G, 8, INLINE><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
+  if (!INLINE && a.split_off[a.batch] > a.batch)
+    decode_merge_kernel<G><<<dim3(a.n_kv, a.batch), block, 0, s>>>(a);
   return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_decode_g(const DecodeArgs &a, hipStream_t s) {
+  return a.merge_inline ? launch_decode_gi<G, true>(a, s) : launch_decode_gi<G, false>(a, s);
 }
 
 }  // namespace
