@@ -129,7 +129,7 @@ struct bnr_ctx {
   int mirror_mode = BNR_MIRROR_INCREMENTAL;
 
   // decode planner
-  int target_wgs = 640;
+  int target_wgs = 160;
   int force_rpg = 0;
   int merge_inline = 1;
 };

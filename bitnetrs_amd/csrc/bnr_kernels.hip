@@ -170,8 +170,10 @@ template <int G, bool AGENT>
 __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, int nsplit,
                                              float *lds) {
   constexpr int D = kHeadDim;
-  constexpr int EPT = (G * D + 255) / 256;  // output elements per lane
-  constexpr int CH = 64 / EPT;              // splits per round (at most one per lane)
+  constexpr int NE = G * D;                 // output elements of this kv head
+  constexpr int EPL = NE >= 512 ? 2 : 1;    // adjacent elements per lane (one 8-byte load)
+  constexpr int NT = NE / EPL;              // lanes with work (<= 256)
+  constexpr int CH = 64;                    // splits per round (one per lane of a wave)
   constexpr int GPW = (G + 3) / 4;          // q heads per wave
   float *s_w = lds;             // [G][CH] split weights of the round
   float *s_M = s_w + CH * G;    // [G] running max
@@ -179,29 +181,36 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
   float *s_sc = s_L + G;        // [G] rescale of the earlier rounds
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int gs0 = a.split_off[b];
-  const long long step = (long long)a.n_kv * G * D;
-  const float *po = a.ws_o + ((long long)gs0 * a.n_kv + h) * G * D;
+  const long long step = (long long)a.n_kv * NE;
+  const float *po = a.ws_o + ((long long)gs0 * a.n_kv + h) * NE;
   if (tid < G) {
     s_M[tid] = -INFINITY;
     s_L[tid] = 0.f;
   }
-  // Lane element k: e = tid + 256k (G == 1: lanes 128..255 shadow 0..127).
-  int ek[EPT];
+  const int e0 = (tid % NT) * EPL;  // first element of this lane (lanes >= NT shadow)
+  const int g0 = e0 / D;
+  float Or[EPL];
 #pragma unroll
-  for (int k = 0; k < EPT; ++k) ek[k] = (tid + 256 * k) % (G * D);
-  float Or[EPT];
-#pragma unroll
-  for (int k = 0; k < EPT; ++k) Or[k] = 0.f;
+  for (int k = 0; k < EPL; ++k) Or[k] = 0.f;
   for (int c0 = 0; c0 < nsplit; c0 += CH) {
     const int n = min(CH, nsplit - c0);
     // One batch of loads; split indices past the end are clamped (their
     // weight is zero), so there are no branches between loads.
-    float ov[EPT][CH];
+    float ov[EPL][CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
-      const float *pu = po + (long long)min(c0 + u, nsplit - 1) * step;
-#pragma unroll
-      for (int k = 0; k < EPT; ++k) ov[k][u] = AGENT ? ld_agent(pu + ek[k]) : pu[ek[k]];
+      const float *pu = po + (long long)min(c0 + u, nsplit - 1) * step + e0;
+      if (EPL == 2) {
+        const unsigned long long r =
+            AGENT ? __hip_atomic_load(reinterpret_cast<const unsigned long long *>(pu),
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                  : *reinterpret_cast<const unsigned long long *>(pu);
+        const float2 f = __builtin_bit_cast(float2, r);
+        ov[0][u] = f.x;
+        ov[EPL - 1][u] = f.y;
+      } else {
+        ov[0][u] = AGENT ? ld_agent(pu) : *pu;
+      }
     }
     float2 mlr[GPW];
 #pragma unroll
@@ -221,7 +230,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
       const float mn = fmaxf(m_old, wave_max(m));
       const float w = lane < n ? fast_exp2(m - mn) : 0.f;
       const float ls = wave_sum(w * mlr[r].y);
-      if (lane < CH) s_w[g * CH + lane] = w;
+      s_w[g * CH + lane] = w;
       if (lane == 0) {
         const float sc = fast_exp2(m_old - mn);  // 0 on the first round
         s_sc[g] = sc;
@@ -230,26 +239,27 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
       }
     }
     __syncthreads();
+    const float4 *w4 = reinterpret_cast<const float4 *>(s_w + g0 * CH);
+    const float sc = s_sc[g0];
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const int g = ek[k] / D;
-      const float4 *w4 = reinterpret_cast<const float4 *>(s_w + g * CH);
-      float o = Or[k] * s_sc[g];
+    for (int k = 0; k < EPL; ++k) Or[k] *= sc;
 #pragma unroll
-      for (int u4 = 0; u4 < CH / 4; ++u4) {
-        const float4 w = w4[u4];
-        o = fmaf(w.x, ov[k][4 * u4 + 0], o);
-        o = fmaf(w.y, ov[k][4 * u4 + 1], o);
-        o = fmaf(w.z, ov[k][4 * u4 + 2], o);
-        o = fmaf(w.w, ov[k][4 * u4 + 3], o);
+    for (int u4 = 0; u4 < CH / 4; ++u4) {
+      const float4 w = w4[u4];
+#pragma unroll
+      for (int k = 0; k < EPL; ++k) {
+        Or[k] = fmaf(w.x, ov[k][4 * u4 + 0], Or[k]);
+        Or[k] = fmaf(w.y, ov[k][4 * u4 + 1], Or[k]);
+        Or[k] = fmaf(w.z, ov[k][4 * u4 + 2], Or[k]);
+        Or[k] = fmaf(w.w, ov[k][4 * u4 + 3], Or[k]);
       }
-      Or[k] = o;
     }
   }
+  if (tid < NT) {
+    const float inv = 1.0f / s_L[g0];
+    float *o = a.out + b * a.out_bstride + (long long)h * NE + e0;
 #pragma unroll
-  for (int k = 0; k < EPT; ++k) {
-    if (tid + 256 * k < G * D)
-      a.out[b * a.out_bstride + (long long)h * G * D + ek[k]] = Or[k] / s_L[ek[k] / D];
+    for (int k = 0; k < EPL; ++k) o[k] = Or[k] * inv;
   }
 }
 
