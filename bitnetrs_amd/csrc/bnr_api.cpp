@@ -798,6 +798,23 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
   hipStream_t s = (hipStream_t)stream;
   const long long qs = (long long)(n_heads * head_dim);
   const long long kv_stride = (long long)(cap * head_dim);
+  const int group = (int)(n_heads / n_kv_heads);
+  if (head_dim == (size_t)kHeadDim && prefill_supported(group) && aligned16(q) &&
+      aligned16(k_cache) && aligned16(v_cache) && aligned16(out)) {
+    PrefillArgs pa{};
+    pa.q = q;
+    pa.k_cache = k_cache;
+    pa.v_cache = v_cache;
+    pa.kv_stride = kv_stride;
+    pa.out = out;
+    pa.n_tokens = (int)n_tokens;
+    pa.start_pos = (int)start_pos;
+    pa.n_heads = (int)n_heads;
+    pa.n_kv = (int)n_kv_heads;
+    pa.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
+    HIP_TRY(launch_prefill(pa, group, s), "prefill launch");
+    return set_ok();
+  }
   if (fast_shape(n_heads, n_kv_heads, head_dim) && aligned16(q) && aligned16(k_cache) &&
       aligned16(v_cache)) {
     // Each query row is a decode over the shared cache at its own position.

@@ -73,4 +73,17 @@ struct DecodeGenericArgs {
 };
 hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s);
 
+// Causal flash prefill (head_dim 128, fp32 MFMA): query i of the n_tokens
+// (position start_pos + i) attends cache rows 0..start_pos+i.
+struct PrefillArgs {
+  const float *q;                    // [n_tokens][n_heads][128], rotated
+  const float *k_cache, *v_cache;    // [n_kv][cap][128]
+  long long kv_stride;               // cap * 128
+  float *out;                        // [n_tokens][n_heads][128]
+  int n_tokens, start_pos, n_heads, n_kv;
+  float scale_log2;                  // log2(e) / sqrt(128)
+};
+hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s);
+bool prefill_supported(int group);
+
 }  // namespace bnr

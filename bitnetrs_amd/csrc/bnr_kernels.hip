@@ -523,6 +523,152 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Causal flash prefill on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// Workgroup = one kv head's G query heads (one wave each) x 32 queries; the
+// G waves share every 32-key K/V tile, staged in LDS (double buffered, rows
+// padded to 132 floats so that the 32 lanes of a half-wave hit distinct
+// banks).  Each wave computes S^T = K Q^T (32 keys x 32 queries), so the
+// accumulator layout of S^T is exactly the B-operand layout P^T needs for
+// O^T = V^T P^T: no transposes, no LDS round trip for P.
+//
+// Lane l of a wave: col = l % 32 is its query, hl = l / 32 its half.  Q
+// fragment: dims 64*hl .. 64*hl+63 of that query (registers, prescaled by
+// log2(e)/sqrt(d)).  MFMA step kk (0..63) uses dim 64*hl + kk for the lane's
+// k-slot, so K rows are read from LDS as contiguous float4s.  Accumulator
+// register r of a 32x32 tile holds row 8*(r/4) + 4*hl + r%4.  Online softmax
+// per query: a key tile's max and sum are the lane's 16 values plus its
+// partner lane l^32.  Query tiles with the most keys are dispatched first.
+// ---------------------------------------------------------------------------
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <int G>
+__global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
+  constexpr int D = kHeadDim, BQ = 32, BK = 32, KP = D + 4, NT = 64 * G;
+  constexpr int F4 = BK * D / 4 / NT;  // float4 of K (and of V) per lane per tile
+  __shared__ float sK[2][BK][KP];
+  __shared__ float sV[2][BK][KP];
+
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int hl = lane >> 5, col = lane & 31;
+  const int h = blockIdx.x;                        // kv head (fastest: longest tiles of
+  const int qt = gridDim.y - 1 - blockIdx.y;       // every head are dispatched first)
+  const int q0 = qt * BQ;
+  const int qrow = min(q0 + col, a.n_tokens - 1);  // rows past the end are not stored
+  const int head = h * G + g;
+  const int last_row = a.start_pos + a.n_tokens - 1;
+  const int pq = a.start_pos + qrow;               // this lane's query position
+  const int kmax = min(a.start_pos + q0 + BQ - 1, last_row);
+  const int nkt = kmax / BK + 1;
+  const float *kc = a.k_cache + h * a.kv_stride;
+  const float *vc = a.v_cache + h * a.kv_stride;
+
+  float4 rk[F4], rv[F4];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+      const int f = tid + NT * i, row = f >> 5, c4 = f & 31;
+      const long long off = (long long)min(kt * BK + row, last_row) * D + 4 * c4;
+      rk[i] = ld4(kc + off);
+      rv[i] = ld4(vc + off);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+      const int f = tid + NT * i, row = f >> 5, c4 = f & 31;
+      st4(&sK[buf][row][4 * c4], rk[i]);
+      st4(&sV[buf][row][4 * c4], rv[i]);
+    }
+  };
+  gload(0);
+
+  float qf[64];
+  {
+    const float *qp = a.q + ((long long)qrow * a.n_heads + head) * D + 64 * hl;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 v = ld4(qp + 4 * i);
+      qf[4 * i] = v.x * a.scale_log2;
+      qf[4 * i + 1] = v.y * a.scale_log2;
+      qf[4 * i + 2] = v.z * a.scale_log2;
+      qf[4 * i + 3] = v.w * a.scale_log2;
+    }
+  }
+  lstore(0);
+  __syncthreads();
+
+  floatx16 O[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+  float m = -INFINITY, l = 0.f;
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt) gload(kt + 1);
+
+    // S^T tile: 32 keys x 32 queries.
+    floatx16 S = floatx16{};
+    const float *krow = &sK[buf][col][64 * hl];
+#pragma unroll
+    for (int kk = 0; kk < 64; kk += 4) {
+      const float4 kv = *reinterpret_cast<const float4 *>(krow + kk);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[kk], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[kk + 1], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[kk + 2], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[kk + 3], S, 0, 0, 0);
+    }
+    const int kbase = kt * BK;
+    if (kbase + BK - 1 > a.start_pos + q0) {  // the tile reaches the causal diagonal
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kbase + 8 * (r >> 2) + 4 * hl + (r & 3);
+        if (key > pq) S[r] = -INFINITY;
+      }
+    }
+    float mb = S[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) mb = fmaxf(mb, S[r]);
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);  // finite: key 0 is visible to every query
+    const float alpha = fast_exp2(m - mn);
+    float p[16], ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp2(S[r] - mn);
+      ls += p[r];
+    }
+    l = fmaf(l, alpha, ls);
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) O[db] *= alpha;
+
+    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile.
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float *vrow = &sV[buf][8 * (s >> 2) + 4 * hl + (s & 3)][col];
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+        O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], p[s], O[db], 0, 0, 0);
+    }
+    if (kt + 1 < nkt) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const float inv = 1.0f / (l + __shfl_xor(l, 32));
+  if (q0 + col < a.n_tokens) {
+    float *op = a.out + ((long long)(q0 + col) * a.n_heads + head) * D + 4 * hl;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+        st4(op + 32 * db + 8 * rq,
+            make_float4(O[db][4 * rq] * inv, O[db][4 * rq + 1] * inv, O[db][4 * rq + 2] * inv,
+                        O[db][4 * rq + 3] * inv));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic decode attention (any head_dim, any group size).  Same three
 // phases as attention::masked_attention (bitnet-cpu/src/attention.rs:
 // 183-204): scores, softmax, weighted sum of V rows.
@@ -615,6 +761,20 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
     case 8: return launch_decode_g<8>(a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool prefill_supported(int group) { return group == 2 || group == 4 || group == 8; }
+
+hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s) {
+  if (a.n_tokens <= 0) return hipSuccess;
+  const dim3 grid(a.n_kv, (a.n_tokens + 31) / 32);
+  switch (group) {
+    case 2: prefill_kernel<2><<<grid, dim3(128), 0, s>>>(a); break;
+    case 4: prefill_kernel<4><<<grid, dim3(256), 0, s>>>(a); break;
+    case 8: prefill_kernel<8><<<grid, dim3(512), 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s) {

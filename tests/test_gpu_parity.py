@@ -314,3 +314,30 @@ def test_dev_argument_errors(backend):
         backend.dev_decode_attention(t, kc, kc, 16, t, 20, 3, D, 0)
     with pytest.raises(bitnetrs_amd.InvalidConfig):
         backend.dev_rope_append(t, t, t, 1, 0, HQ, HKV, D, -1.0, kc, kc, 16)
+
+
+@pytest.mark.parametrize("n_heads,n_kv,n_tokens,start", [(20, 5, 33, 0), (20, 5, 1, 0),
+                                                        (20, 5, 64, 31), (16, 2, 70, 5),
+                                                        (8, 4, 40, 0), (8, 8, 20, 3)])
+def test_dev_prefill_shapes(backend, n_heads, n_kv, n_tokens, start):
+    case(f"prefill heads {n_heads}/{n_kv} n {n_tokens} start {start}")
+    import torch
+
+    cap = start + n_tokens + 7
+    cache = oracle.KVCache(1, n_kv, D, cap)
+    be = oracle.CpuBackend()
+    d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+    d_vc = torch.zeros_like(d_kc)
+    if start:
+        pre = prefill_workload(34, start, n_heads, n_kv)
+        oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+    w = prefill_workload(35, n_tokens, n_heads, n_kv)
+    q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
+                                                  n_heads=n_heads, n_kv=n_kv)
+    out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+    backend.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads, n_kv, D,
+                        THETA, d_kc, d_vc, cap, out)
+    np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+    assert_close(host(out), out_ref, f"prefill {n_heads}/{n_kv} n {n_tokens}")
