@@ -65,7 +65,7 @@ def per_launch_ms(torch, launch, n: int) -> float:
     return sum(ds) / len(ds)
 
 
-def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32):
+def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: bool = False):
     L, pos, cap = 4096, 4095, 4096
     g = torch.Generator(device="cuda").manual_seed(0xB17E7020)
     kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
@@ -87,6 +87,8 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32):
     # overhead; the GPU still runs K separate kernels).
     graph = None
     try:
+        if eager:
+            raise RuntimeError("eager timing requested")
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -115,12 +117,17 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32):
     torch.cuda.synchronize()
     ms_total = t0.elapsed_time(t1)
     ms_step = ms_total / steps
-    kernel_ms = per_launch_ms(torch, step, min(steps, 200))
+    # One decode_kernel launch per step: inside the graph the per-step time is
+    # the kernel's duration plus the dispatch gap between graph nodes.  The
+    # event-pair figure (spin-held queue) is reported beside it.
+    kernel_ms = ms_step if graph is not None else per_launch_ms(torch, step, min(steps, 200))
+    pair_ms = per_launch_ms(torch, step, min(steps, 200))
     nbytes = decode_bytes(L)
     res = {
         "ms_per_step": ms_step,
         "gbs": nbytes / (ms_step * 1e-3) / 1e9,
         "kernel_ms": kernel_ms,
+        "pair_ms": pair_ms,
         "kernel_gbs": nbytes / (kernel_ms * 1e-3) / 1e9,
         "bytes_per_step": nbytes,
         "graph": graph is not None,
@@ -168,6 +175,28 @@ def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048, n_layers: i
     return {"ms_per_step": ms_step, "tflops": flops / (ms_step * 1e-3) / 1e12,
             "attn_ms": attn_ms, "attn_tflops": flops / (attn_ms * 1e-3) / 1e12,
             "flops": flops}
+
+
+def copy_calibration(torch, nbytes: int = 256 << 20, reps: int = 5) -> None:
+    """Plain device-to-device copies of a known size: the reference for
+    scaling FETCH_SIZE / WRITE_SIZE counters in a --pmc run of this script."""
+    src = torch.empty(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {reps} copies of {nbytes} bytes")
+
+
+def load_traffic():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by the copy calibration), if recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
 
 
 def cpu_baseline_decode(host, budget_s: float):
@@ -232,6 +261,10 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of a captured graph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run plain copies of a known size (for --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -245,9 +278,13 @@ def main() -> int:
 
     be = bitnetrs_amd.HipBackend(0)
     log(f"device: {be.device_name()}")
-    dec = bench_decode(torch, be, args.steps, args.warmup)
+    if args.copy_calibration:
+        copy_calibration(torch)
+    traffic = load_traffic()
+    dec = bench_decode(torch, be, args.steps, args.warmup, eager=args.eager)
     log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step, {dec['gbs']:.0f} GB/s; kernel "
-        f"{dec['kernel_ms'] * 1e3:.2f} us, {dec['kernel_gbs']:.0f} GB/s")
+        f"{dec['kernel_ms'] * 1e3:.2f} us, {dec['kernel_gbs']:.0f} GB/s; event pair "
+        f"{dec['pair_ms'] * 1e3:.2f} us")
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 2),
@@ -267,8 +304,10 @@ def main() -> int:
                    "timed": "hip graph of fused rope+append+split-K attention launches"},
         "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("decode_kernel", {}).get("bytes_per_launch"),
                      "kernel": "decode_kernel", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
+                     "event_pair_us": round(dec["pair_ms"] * 1e3, 3),
                      "bytes_per_launch": dec["bytes_per_step"]},
     }
     if not args.no_prefill:
@@ -282,7 +321,9 @@ def main() -> int:
             "roofline": {"bound": "mfma", "achieved": round(pre["attn_tflops"], 3),
                          "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["attn_tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4),
-                         "traffic": None, "flops_per_launch": pre["flops"]},
+                         "traffic": traffic.get("prefill_kernel", {}).get("bytes_per_launch"),
+                         "kernel": "prefill_kernel", "kernel_us": round(pre["attn_ms"] * 1e3, 3),
+                         "flops_per_launch": pre["flops"]},
         }
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
