@@ -177,6 +177,58 @@ def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048, n_layers: i
             "flops": flops}
 
 
+def bench_stack(torch, be, n_layers: int = 30, n_pre: int = 1024, n_dec: int = 256):
+    """The 30-layer stack at the 2B shape: 1024-token causal prefill of every
+    layer, then 256 decode steps (every layer each step), seeded N(0,1)
+    projections per layer and step.  Decode is timed as one HIP graph of
+    all n_layers * n_dec fused decode launches."""
+    import bitnetrs_amd
+
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7050)
+    qp = torch.randn(n_layers, n_pre, HQ * D, device="cuda", generator=g)
+    kp = torch.randn(n_layers, n_pre, HKV * D, device="cuda", generator=g)
+    vp = torch.randn(n_layers, n_pre, HKV * D, device="cuda", generator=g)
+    qd = torch.randn(n_dec, n_layers, HQ * D, device="cuda", generator=g)
+    kd = torch.randn(n_dec, n_layers, HKV * D, device="cuda", generator=g)
+    vd = torch.randn(n_dec, n_layers, HKV * D, device="cuda", generator=g)
+    out_p = torch.zeros_like(qp)
+    out_d = torch.zeros_like(qd)
+    st = bitnetrs_amd.AttentionStack(be, n_layers, HQ, HKV, D, n_pre + n_dec, THETA)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    st.prefill(qp, kp, vp, out_p)
+    t1.record()
+    torch.cuda.synchronize()
+    pre_ms = t0.elapsed_time(t1)
+    start = st.position
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # one eager step on a side stream before capture
+        st.decode(qd[0], kd[0], vd[0], out_d[0])
+    torch.cuda.current_stream().wait_stream(side)
+    st.cache.filled_positions = start
+    st.cache.layer_lengths = [start] * n_layers
+    with torch.cuda.graph(graph):
+        for s in range(n_dec):
+            st.decode(qd[s], kd[s], vd[s], out_d[s])
+    graph.replay()  # first replay writes the cache rows; replays are idempotent
+    torch.cuda.synchronize()
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    dec_ms = t0.elapsed_time(t1)
+    dec_bytes = n_layers * sum(decode_bytes(n_pre + s + 1) for s in range(n_dec))
+    pre_flops = n_layers * prefill_flops(n_pre)
+    return {"prefill_ms": pre_ms, "prefill_tflops": pre_flops / (pre_ms * 1e-3) / 1e12,
+            "decode_ms": dec_ms, "decode_gbs": dec_bytes / (dec_ms * 1e-3) / 1e9,
+            "decode_tok_s": n_dec / (dec_ms * 1e-3), "decode_bytes": dec_bytes,
+            "prefill_flops": pre_flops, "launches": n_layers * n_dec}
+
+
 def copy_calibration(torch, nbytes: int = 256 << 20, reps: int = 5) -> None:
     """Plain device-to-device copies of a known size: the reference for
     scaling FETCH_SIZE / WRITE_SIZE counters in a --pmc run of this script."""
@@ -260,6 +312,7 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack workload")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -325,6 +378,19 @@ def main() -> int:
                          "kernel": "prefill_kernel", "kernel_us": round(pre["attn_ms"] * 1e3, 3),
                          "flops_per_launch": pre["flops"]},
         }
+    if not args.no_stack:
+        stk = bench_stack(torch, be)
+        log(f"stack: prefill 30x1024 {stk['prefill_ms']:.2f} ms ({stk['prefill_tflops']:.1f} TFLOP/s); "
+            f"decode 256 steps x 30 layers {stk['decode_ms']:.2f} ms ({stk['decode_gbs']:.0f} GB/s, "
+            f"{stk['decode_tok_s']:.0f} tok/s attention-only)")
+        line["stack"] = {
+            "workload": "bitnet_2b_attention_stack_30L_prefill1024_decode256_fp32",
+            "prefill_ms": round(stk["prefill_ms"], 3), "prefill_tflops": round(stk["prefill_tflops"], 2),
+            "decode_ms": round(stk["decode_ms"], 3), "decode_gbs": round(stk["decode_gbs"], 1),
+            "decode_tok_s": round(stk["decode_tok_s"], 1), "decode_bytes": stk["decode_bytes"],
+            "prefill_flops": stk["prefill_flops"],
+            "note": "decode timed as one HIP graph of 7680 fused decode launches; caches total "
+                    "197 MB, which fits the 256 MB MALL"}
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)

@@ -6,9 +6,10 @@ kernels behind the C ABI in ``include/bitnet_hip.h``.  ``HipBackend`` mirrors
 the reference's ``Backend::rope_embed`` / ``Backend::masked_attention``.
 """
 from ._lib import LIB_PATH, build, load
+from .stack import AttentionStack
 from .backend import (BNR_MIRROR_FULL, BNR_MIRROR_INCREMENTAL, BackendError, BitNetError,
                       DeviceKVCache, HipBackend, InvalidConfig, InvalidShape, UnsupportedDevice)
 
-__all__ = ["HipBackend", "DeviceKVCache", "BitNetError", "InvalidShape", "InvalidConfig",
+__all__ = ["HipBackend", "DeviceKVCache", "AttentionStack", "BitNetError", "InvalidShape", "InvalidConfig",
            "BackendError", "UnsupportedDevice", "BNR_MIRROR_FULL", "BNR_MIRROR_INCREMENTAL",
            "build", "load", "LIB_PATH"]

@@ -281,7 +281,7 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
 // Launch the fast decode kernel over `batch` (<= kMaxBatchPerLaunch)
 // sequences; a.{q,k_new,...,strides} are filled by the caller.
 int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n_kv, int group,
-               hipStream_t s) {
+               size_t cap, hipStream_t s) {
   int lens[kMaxBatchPerLaunch];
   for (int b = 0; b < batch; ++b) {
     lens[b] = positions[b] + 1;
@@ -292,7 +292,11 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
   a.group = group;
   a.merge_inline = c->merge_inline;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
-  const size_t splits = (size_t)a.split_off[batch];
+  // Size the workspace for the most splits any position below `cap` can
+  // need, so that later calls on the same caches -- including calls under
+  // HIP graph capture -- never allocate.
+  const size_t worst = std::min<size_t>(kMaxSplits, (cap + 15) / 16);
+  const size_t splits = std::max<size_t>((size_t)a.split_off[batch], worst * (size_t)batch);
   int st = ensure_ws(c, splits * n_kv * group * kHeadDim, splits * n_kv * group);
   if (st) return st;
   st = ensure_counters(c, (size_t)batch * n_kv * kCounterStride);
@@ -538,7 +542,7 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     a.kv_stride = kv_stride;
     a.out = c->d_out;
     const int p = (int)cur_pos;
-    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), c->stream);
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), m->rows, c->stream);
   } else {
     st = run_generic(c, c->d_q, m->dk, m->dv, kv_stride, c->d_out, n_heads, n_kv_heads, head_dim,
                      cur_pos, c->stream);
@@ -668,7 +672,7 @@ extern "C" int bnr_dev_decode_attention(bnr_ctx *c, const float *q, const float 
     a.kv_stride = kv_stride;
     a.out = out;
     const int p = (int)cur_pos;
-    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), cap, s);
   } else {
     st = run_generic(c, q, k_cache, v_cache, kv_stride, out, n_heads, n_kv_heads, head_dim, cur_pos, s);
   }
@@ -708,7 +712,7 @@ extern "C" int bnr_dev_decode_step(bnr_ctx *c, const float *q, const float *k, c
     a.cos_tab = c->d_cos;
     a.sin_tab = c->d_sin;
     const int p = (int)position;
-    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), cap, s);
     return st ? st : set_ok();
   }
   // Any other shape: rotate copies, append, then the generic kernel.
@@ -776,7 +780,8 @@ extern "C" int bnr_dev_decode_step_batched(bnr_ctx *c, const float *q, const flo
     a.out = out + b0 * qs;
     a.cos_tab = c->d_cos;
     a.sin_tab = c->d_sin;
-    st = run_decode(c, a, positions + b0, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+    st = run_decode(c, a, positions + b0, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), cap,
+                    s);
     if (st) return st;
   }
   return set_ok();
@@ -830,7 +835,7 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
       a.out_bstride = qs;
       a.kv_stride = kv_stride;
       a.out = out + t0 * qs;
-      st = run_decode(c, a, pos, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), s);
+      st = run_decode(c, a, pos, nb, (int)n_kv_heads, (int)(n_heads / n_kv_heads), cap, s);
       if (st) return st;
     }
     return set_ok();
