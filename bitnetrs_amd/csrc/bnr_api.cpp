@@ -275,7 +275,12 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
   a.rows_per_split = rows;
   a.batch = batch;
   a.split_off[0] = 0;
-  for (int b = 0; b < batch; ++b) a.split_off[b + 1] = a.split_off[b] + (lens[b] + rows - 1) / rows;
+  a.max_splits = 1;
+  for (int b = 0; b < batch; ++b) {
+    const int ns = (lens[b] + rows - 1) / rows;
+    a.split_off[b + 1] = a.split_off[b] + ns;
+    a.max_splits = std::max(a.max_splits, ns);
+  }
 }
 
 // Launch the fast decode kernel over `batch` (<= kMaxBatchPerLaunch)

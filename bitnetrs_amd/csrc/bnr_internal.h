@@ -55,6 +55,7 @@ struct DecodeArgs {
   int rpg;                        // rows per 16-lane row group and pass
   int passes;
   int merge_inline;                // 1: last-workgroup merge; 0: second kernel
+  int max_splits;                  // largest split count of the launch (grid x)
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
 };

@@ -284,23 +284,27 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
 // splits) and writes the output.  It also resets the ticket counter, so no
 // memset is needed between launches.
 // ---------------------------------------------------------------------------
-template <int G, int RPG, bool INLINE>
+template <int G, int RPG, bool INLINE, bool RAGGED>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   __shared__ float s_o[16][G][D];
   __shared__ float s_m[G][16];
   __shared__ float s_l[G][16];
+  __shared__ float s_w[G][16];
+  __shared__ float s_M[G], s_L[G];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int rg = tid >> 4;
   const int j = tid & 15;
 
-  // blockIdx.x -> (sequence b, split s); the table is in kernel arguments.
-  int b = 0;
-  while ((int)blockIdx.x >= a.split_off[b + 1]) ++b;
-  const int s = (int)blockIdx.x - a.split_off[b];
+  // Grid (max splits, kv heads, sequences): every kernel argument this
+  // workgroup needs is fetched in one batch (no dependent lookups); splits
+  // past a shorter sequence's count exit at once.
+  const int b = blockIdx.z;
+  const int s = blockIdx.x;
   const int nsplit = a.split_off[b + 1] - a.split_off[b];
+  if (RAGGED && s >= nsplit) return;  // only when sequences differ in split count
   const int h = blockIdx.y;
   const int pos = a.positions[b];
   const int L = pos + 1;
@@ -456,29 +460,40 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   }
   __syncthreads();
 
+  // Row-group weights once per (q head, row group): lane 16g + r of wave 0
+  // takes row group r of head g; a DPP row is one head.
+  if (tid < 64) {
+#pragma unroll
+    for (int g0 = 0; g0 < G; g0 += 4) {
+      const int g = g0 + (tid >> 4), r = tid & 15;
+      if (g < G) {
+        const float mr = s_m[g][r];
+        const float M = row_max16(mr);
+        const float w = fast_exp2(mr - M);  // 0 for an empty row group
+        const float Ls = row_sum16(s_l[g][r] * w);
+        s_w[g][r] = w;
+        if (r == 0) {
+          s_M[g] = M;
+          s_L[g] = Ls;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
   const int gs = a.split_off[b] + s;  // global split index
   for (int e = tid; e < G * D; e += 256) {
     const int g = e / D, dim = e % D;
-    float mr[16], lr[16], orr[16];
+    float O = 0.f;
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const float4 m4 = *reinterpret_cast<const float4 *>(&s_m[g][4 * r4]);
-      const float4 l4 = *reinterpret_cast<const float4 *>(&s_l[g][4 * r4]);
-      mr[4 * r4] = m4.x, mr[4 * r4 + 1] = m4.y, mr[4 * r4 + 2] = m4.z, mr[4 * r4 + 3] = m4.w;
-      lr[4 * r4] = l4.x, lr[4 * r4 + 1] = l4.y, lr[4 * r4 + 2] = l4.z, lr[4 * r4 + 3] = l4.w;
+      const float4 w4 = *reinterpret_cast<const float4 *>(&s_w[g][4 * r4]);
+      O = fmaf(w4.x, s_o[4 * r4][g][dim], O);
+      O = fmaf(w4.y, s_o[4 * r4 + 1][g][dim], O);
+      O = fmaf(w4.z, s_o[4 * r4 + 2][g][dim], O);
+      O = fmaf(w4.w, s_o[4 * r4 + 3][g][dim], O);
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) orr[r] = s_o[r][g][dim];
-    float M = mr[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) M = fmaxf(M, mr[r]);
-    float Ls = 0.f, O = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float w = fast_exp2(mr[r] - M);  // 0 for an empty row group
-      Ls = fmaf(lr[r], w, Ls);
-      O = fmaf(orr[r], w, O);
-    }
+    const float M = s_M[g], Ls = s_L[g];
     if (nsplit == 1) {
       a.out[b * a.out_bstride + ((long long)h * G + g) * D + dim] = O / Ls;
     } else if (INLINE) {
@@ -511,15 +526,63 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   merge_splits<G, true>(a, b, h, nsplit, &s_o[0][0][0]);
 }
 
-// Second kernel of the two-launch decode: one workgroup per (kv head,
-// sequence) merges the split partials written by decode_kernel<.., false>.
+// Second kernel of the two-launch decode: one workgroup of 256 lanes per
+// (sequence, kv head, q head) merges that q head's split partials, written by
+// decode_kernel<.., false> (the kernel boundary makes them visible; plain
+// loads).  Lane t loads the (max, sum) of split t; the split weights come from
+// a block max; lane (d, p) = (t % 128, t / 128) accumulates the splits of
+// parity p for output dim d, all loads of a round in flight together.
 template <int G>
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-  __shared__ float lds[64 * G + 3 * G];
-  const int h = blockIdx.x, b = blockIdx.y;
+  constexpr int D = kHeadDim, CH = 32;
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[8];
+  __shared__ float s_o[D];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int h = blockIdx.x / G, g = blockIdx.x % G, b = blockIdx.y;
   const int nsplit = a.split_off[b + 1] - a.split_off[b];
   if (nsplit == 1) return;
-  merge_splits<G, false>(a, b, h, nsplit, lds);
+  const int gs0 = a.split_off[b];
+  const long long step = (long long)a.n_kv * G * D;
+  const float *po = a.ws_o + ((long long)gs0 * a.n_kv + h) * G * D + g * D;
+  const int d = tid & (D - 1), par = tid >> 7;
+
+  // Split partials of this lane (parity par), first round, issued with the
+  // (max, sum) loads so that both arrive in one round trip.
+  float ov[CH];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) ov[u] = po[(long long)min(2 * u + par, nsplit - 1) * step + d];
+  float2 ml = make_float2(-INFINITY, 0.f);
+  if (tid < nsplit) ml = a.ws_ml[((long long)(gs0 + tid) * a.n_kv + h) * G + g];
+
+  // Block max of the split maxima.
+  const float wm = wave_max(ml.x);
+  if (lane == 0) s_red[wv] = wm;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float w = tid < nsplit ? fast_exp2(ml.x - M) : 0.f;
+  if (tid < nsplit) s_w[tid] = w;
+  const float wl = wave_sum(w * ml.y);
+  if (lane == 0) s_red[4 + wv] = wl;
+  __syncthreads();
+  const float Ls = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
+
+  float o = 0.f;
+  for (int c0 = 0; c0 < nsplit; c0 += 2 * CH) {
+    if (c0 > 0) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u)
+        ov[u] = po[(long long)min(c0 + 2 * u + par, nsplit - 1) * step + d];
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int sp = c0 + 2 * u + par;
+      if (sp < nsplit) o = fmaf(s_w[sp], ov[u], o);
+    }
+  }
+  if (par == 1) s_o[d] = o;
+  __syncthreads();
+  if (par == 0) a.out[b * a.out_bstride + ((long long)h * G + g) * D + d] = (o + s_o[d]) / Ls;
 }
 
 // ---------------------------------------------------------------------------
@@ -722,19 +785,28 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeGenericArgs a
   }
 }
 
-template <int G, bool INLINE>
-hipError_t launch_decode_gi(const DecodeArgs &a, hipStream_t s) {
-  dim3 grid(a.split_off[a.batch], a.n_kv), block(256);
+template <int G, bool INLINE, bool RAGGED>
+hipError_t launch_decode_gir(const DecodeArgs &a, hipStream_t s) {
+  dim3 grid(a.max_splits, a.n_kv, a.batch), block(256);
   switch (a.rpg) {
-    case 1: decode_kernel<G, 1, INLINE><<<grid, block, 0, s>>>(a); break;
-    case 2: decode_kernel<G, 2, INLINE><<<grid, block, 0, s>>>(a); break;
-    case 4: decode_kernel<G, 4, INLINE><<<grid, block, 0, s>>>(a); break;
-    case 8: decode_kernel<G, 8, INLINE><<<grid, block, 0, s>>>(a); break;
+    case 1: decode_kernel<G, 1, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 2: decode_kernel<G, 2, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 4: decode_kernel<G, 4, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 8: decode_kernel<G, 8, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
-  if (!INLINE && a.split_off[a.batch] > a.batch)
-    decode_merge_kernel<G><<<dim3(a.n_kv, a.batch), block, 0, s>>>(a);
+  if (!INLINE && a.max_splits > 1)
+    decode_merge_kernel<G><<<dim3(a.n_kv * G, a.batch), block, 0, s>>>(a);
   return hipGetLastError();
+}
+
+template <int G, bool INLINE>
+hipError_t launch_decode_gi(const DecodeArgs &a, hipStream_t s) {
+  // Uniform split counts (always so for one sequence): no early-exit check.
+  bool ragged = false;
+  for (int b = 0; b < a.batch; ++b)
+    ragged |= (a.split_off[b + 1] - a.split_off[b]) != a.max_splits;
+  return ragged ? launch_decode_gir<G, INLINE, true>(a, s) : launch_decode_gir<G, INLINE, false>(a, s);
 }
 
 template <int G>
