@@ -229,6 +229,46 @@ def bench_stack(torch, be, n_layers: int = 30, n_pre: int = 1024, n_dec: int = 2
             "prefill_flops": pre_flops, "launches": n_layers * n_dec}
 
 
+def bench_batched(torch, be, steps: int = 50, n_seq: int = 32, cap: int = 4096):
+    """32 independent sequences, cached lengths ~ U[128, 4096) (seeded), one
+    fused decode step each per launch (ragged split-K)."""
+    import numpy as np
+
+    lens = np.random.default_rng(0xB17E7040).integers(128, 4096, size=n_seq).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7041)
+    kc = torch.randn(n_seq, HKV, cap, D, device="cuda", generator=g)
+    vc = torch.randn(n_seq, HKV, cap, D, device="cuda", generator=g)
+    q = torch.randn(n_seq, HQ * D, device="cuda", generator=g)
+    k = torch.randn(n_seq, HKV * D, device="cuda", generator=g)
+    v = torch.randn(n_seq, HKV * D, device="cuda", generator=g)
+    out = torch.zeros(n_seq, HQ * D, device="cuda")
+
+    def step(i):
+        be.dev_decode_step_batched(q, k, v, lens, HQ, HKV, D, THETA, kc, vc, cap, out)
+
+    for i in range(5):
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    nbytes = int(sum(decode_bytes(int(L) + 1) for L in lens))
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
+            "lengths_min_max_mean": [int(lens.min()), int(lens.max()), float(lens.mean())]}
+
+
 def copy_calibration(torch, nbytes: int = 256 << 20, reps: int = 5) -> None:
     """Plain device-to-device copies of a known size: the reference for
     scaling FETCH_SIZE / WRITE_SIZE counters in a --pmc run of this script."""
@@ -313,6 +353,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack workload")
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -378,6 +419,15 @@ def main() -> int:
                          "kernel": "prefill_kernel", "kernel_us": round(pre["attn_ms"] * 1e3, 3),
                          "flops_per_launch": pre["flops"]},
         }
+    if not args.no_batched:
+        bat = bench_batched(torch, be)
+        log(f"batched decode (32 seqs, ragged): {bat['ms_per_step'] * 1e3:.2f} us/step, "
+            f"{bat['gbs']:.0f} GB/s")
+        line["batched"] = {
+            "workload": "gqa_decode_step_batch32_ragged_len_U128_4096_hq20_hkv5_d128_fp32",
+            "value": round(bat["gbs"], 2), "unit": "GB/s", "ms_per_step": bat["ms_per_step"],
+            "bytes_per_step": bat["bytes"], "frac_hbm": round(bat["gbs"] / HBM_PEAK_GBS, 4),
+            "lengths_min_max_mean": bat["lengths_min_max_mean"]}
     if not args.no_stack:
         stk = bench_stack(torch, be)
         log(f"stack: prefill 30x1024 {stk['prefill_ms']:.2f} ms ({stk['prefill_tflops']:.1f} TFLOP/s); "

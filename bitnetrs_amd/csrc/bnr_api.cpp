@@ -130,8 +130,9 @@ struct bnr_ctx {
 
   // decode planner
   int target_wgs = 160;
+  int large_wgs = 1024;
   int force_rpg = 0;
-  int merge_inline = 1;
+  int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel
 };
 
 namespace {
@@ -254,8 +255,19 @@ bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
 void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeArgs &a) {
   static const int rpgs[4] = {8, 4, 2, 1};
   int rpg = 1;
+  long long wgs4 = 0;  // workgroups at 64 rows each
+  for (int b = 0; b < batch; ++b) wgs4 += (lens[b] + 63) / 64;
+  wgs4 *= n_kv;
+  // Large launches (several workgroups per CU): 64-row splits, merged by a
+  // second kernel, so that workgroups never wait on their partial stores.
+  // Small launches: the fewest splits that still give about target_wgs
+  // workgroups, merged in-kernel by the last workgroup.
+  const bool large = wgs4 >= c->large_wgs;
+  a.merge_inline = c->merge_mode >= 0 ? c->merge_mode : (large ? 0 : 1);
   if (c->force_rpg) {
     rpg = c->force_rpg;
+  } else if (large) {
+    rpg = 4;
   } else {
     for (int r : rpgs) {
       long long wgs = 0;
@@ -295,7 +307,6 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
   plan_decode(c, lens, batch, n_kv, a);
   a.n_kv = n_kv;
   a.group = group;
-  a.merge_inline = c->merge_inline;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
   // Size the workspace for the most splits any position below `cap` can
   // need, so that later calls on the same caches -- including calls under
@@ -386,7 +397,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     return err_hip(e, "hipStreamCreate");
   }
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
-  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_inline = atoi(v) != 0;
+  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = atoi(v) != 0;
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
     if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;
