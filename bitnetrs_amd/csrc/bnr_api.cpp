@@ -119,6 +119,10 @@ struct bnr_ctx {
   size_t n_counters = 0;
   float *scratch = nullptr;  // generic-kernel scores and host-path staging
   size_t scratch_floats = 0;
+  float *pf_ws = nullptr;  // prefill chunk partials
+  size_t pf_ws_floats = 0;
+  unsigned *pf_counters = nullptr;
+  size_t n_pf_counters = 0;
 
   // host-path staging
   float *d_q = nullptr, *d_k = nullptr, *d_out = nullptr;
@@ -133,6 +137,12 @@ struct bnr_ctx {
   int large_wgs = 1024;
   int force_rpg = 0;
   int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel
+
+  // prefill planner
+  int n_cu = 256;
+  int pf_chunk_shift = -1;  // -1: planner decides; else key tiles per chunk = 2^shift
+  int pf_plan_key[3] = {-1, -1, -1};  // (n_tokens, start_pos, n_kv) of the last plan
+  int pf_plan_shift = 20;
 };
 
 namespace {
@@ -158,20 +168,24 @@ int ensure_buf(float **p, size_t *cap, size_t n, const char *what) {
   return BNR_OK;
 }
 
-int ensure_counters(bnr_ctx *c, size_t n) {
-  if (c->n_counters >= n && c->counters) return BNR_OK;
-  if (c->counters) {
+// Grow-only, zero-filled ticket counters (kernels leave them zero).
+int ensure_zeroed(unsigned **p, size_t *cap, size_t n) {
+  if (*cap >= n && *p) return BNR_OK;
+  if (*p) {
     (void)hipDeviceSynchronize();
-    (void)hipFree(c->counters);
-    c->counters = nullptr;
+    (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
   }
   size_t want = std::max<size_t>(n, 4096);
-  HIP_TRY(hipMalloc((void **)&c->counters, want * sizeof(unsigned)), "counter alloc");
-  HIP_TRY(hipMemset(c->counters, 0, want * sizeof(unsigned)), "counter clear");
+  HIP_TRY(hipMalloc((void **)p, want * sizeof(unsigned)), "counter alloc");
+  HIP_TRY(hipMemset(*p, 0, want * sizeof(unsigned)), "counter clear");
   HIP_TRY(hipDeviceSynchronize(), "counter clear");
-  c->n_counters = want;
+  *cap = want;
   return BNR_OK;
 }
+
+int ensure_counters(bnr_ctx *c, size_t n) { return ensure_zeroed(&c->counters, &c->n_counters, n); }
 
 int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
   int st = ensure_buf(&c->ws_o, &c->ws_o_floats, o_floats, "workspace alloc");
@@ -187,6 +201,72 @@ int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
     c->ws_ml_n = want;
   }
   return BNR_OK;
+}
+
+// Prefill key-range chunking.  The launch's workgroups (one per CU at this
+// kernel's register use) go to the XCDs round-robin, WG i to XCD i % n_xcd,
+// and in order; a query tile with nk key tiles costs nk tile-times, plus a
+// fixed cost per workgroup (queries and first tile loaded, outputs stored),
+// plus a partial-state store when it is split and a read per merged chunk
+// for the last chunk to finish.  The planner replays that dispatch for each
+// candidate chunk size and keeps the shortest span.  Constants are in units
+// of one 32-key tile of 4 heads (measured: fixed cost ~1.8 tiles, partial
+// store ~1.8 tiles, merge read ~0.06 tiles per chunk).
+double prefill_span(int n_tokens, int start_pos, int n_kv, int shift, int n_cu) {
+  constexpr double kFixed = 1.8, kStore = 1.8, kMerge = 0.06;
+  constexpr int kXcd = 8;
+  const int per_xcd = std::max(1, n_cu / kXcd);
+  std::vector<std::vector<double>> heaps(kXcd, std::vector<double>(per_xcd, 0.0));
+  std::vector<double> chunk_end((size_t)n_kv);
+  const int last_row = start_pos + n_tokens - 1, nqt = (n_tokens + 31) / 32;
+  const int ctiles = 1 << std::min(shift, 20);
+  auto later = [](double a, double b) { return a > b; };  // min-heaps
+  double span = 0.0, t_last = 0.0;
+  long long wg = 0;
+  for (int qt = nqt - 1; qt >= 0; --qt) {
+    const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
+    const int nch = (nk + ctiles - 1) / ctiles;
+    std::fill(chunk_end.begin(), chunk_end.end(), 0.0);
+    for (int ch = 0; ch < nch; ++ch) {
+      const int t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
+      for (int h = 0; h < n_kv; ++h, ++wg) {
+        std::vector<double> &hp = heaps[(size_t)(wg % kXcd)];
+        std::pop_heap(hp.begin(), hp.end(), later);
+        const double start = std::max(hp.back(), t_last);
+        t_last = start;
+        const double end = start + kFixed + t + (nch > 1 ? kStore : 0.0);
+        hp.back() = end;
+        std::push_heap(hp.begin(), hp.end(), later);
+        chunk_end[(size_t)h] = std::max(chunk_end[(size_t)h], end);
+        span = std::max(span, end);
+      }
+    }
+    if (nch > 1)
+      for (int h = 0; h < n_kv; ++h)
+        span = std::max(span, chunk_end[(size_t)h] + (nch - 1) * kMerge);
+  }
+  return span;
+}
+
+int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
+  if (c->pf_plan_key[0] == n_tokens && c->pf_plan_key[1] == start_pos &&
+      c->pf_plan_key[2] == n_kv)
+    return c->pf_plan_shift;
+  int best = 20;
+  double best_span = prefill_span(n_tokens, start_pos, n_kv, 20, c->n_cu);
+  for (int shift = 2; shift <= 6; ++shift) {
+    if (prefill_plan(n_tokens, start_pos, shift).n_items * (long long)n_kv > 16384) continue;
+    const double span = prefill_span(n_tokens, start_pos, n_kv, shift, c->n_cu);
+    if (span < best_span * 0.99) {
+      best_span = span;
+      best = shift;
+    }
+  }
+  c->pf_plan_key[0] = n_tokens;
+  c->pf_plan_key[1] = start_pos;
+  c->pf_plan_key[2] = n_kv;
+  c->pf_plan_shift = best;
+  return best;
 }
 
 // RopeCache::new (bitnet-cpu/src/rope.rs:100-153) on the host: same f32
@@ -402,6 +482,8 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     int r = atoi(v);
     if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;
   }
+  if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
+  if (const char *v = std::getenv("BNR_PREFILL_CHUNK_SHIFT")) c->pf_chunk_shift = std::min(std::max(atoi(v), 0), 20);
   *out = c;
   return set_ok();
 }
@@ -413,11 +495,12 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
     for (auto &m : c->mirrors) free_mirror(m);
-    float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out};
+    float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out, c->pf_ws};
     for (float *p : bufs)
       if (p) (void)hipFree(p);
     if (c->ws_ml) (void)hipFree(c->ws_ml);
     if (c->counters) (void)hipFree(c->counters);
+    if (c->pf_counters) (void)hipFree(c->pf_counters);
     if (c->stream) (void)hipStreamDestroy(c->stream);
   }
   delete c;
@@ -833,6 +916,24 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
     pa.n_heads = (int)n_heads;
     pa.n_kv = (int)n_kv_heads;
     pa.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
+    pa.n_qtiles = (int)((n_tokens + 31) / 32);
+    pa.chunk_shift = c->pf_chunk_shift >= 0
+                         ? c->pf_chunk_shift
+                         : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads);
+    PrefillPlan plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_shift);
+    while (plan.n_items > 65535)  // grid y limit
+      plan = prefill_plan((int)n_tokens, (int)start_pos, ++pa.chunk_shift);
+    pa.n_items = plan.n_items;
+    if (plan.split) {
+      st = ensure_buf(&c->pf_ws, &c->pf_ws_floats,
+                      (size_t)n_kv_heads * plan.n_items * group * 66 * 64, "prefill workspace alloc");
+      if (st) return st;
+      st = ensure_zeroed(&c->pf_counters, &c->n_pf_counters,
+                         (size_t)n_kv_heads * pa.n_qtiles * kCounterStride);
+      if (st) return st;
+      pa.ws = c->pf_ws;
+      pa.counters = c->pf_counters;
+    }
     HIP_TRY(launch_prefill(pa, group, s), "prefill launch");
     return set_ok();
   }

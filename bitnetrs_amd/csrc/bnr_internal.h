@@ -83,7 +83,22 @@ struct PrefillArgs {
   float *out;                        // [n_tokens][n_heads][128]
   int n_tokens, start_pos, n_heads, n_kv;
   float scale_log2;                  // log2(e) / sqrt(128)
+  // Key-range split: a query tile's key tiles are processed in chunks of
+  // 2^chunk_shift tiles by separate workgroups; the last to finish merges.
+  int chunk_shift;
+  int n_qtiles;                      // ceil(n_tokens / 32)
+  int n_items;                       // (query tile, chunk) items per kv head
+  float *ws;                         // partial states: [n_kv][n_items][G][66][64]
+  unsigned *counters;                // [n_kv][n_qtiles] x kCounterStride, zero between launches
 };
+// (query tile, chunk) items per kv head of a prefill launch, and the key
+// tiles they cover in total.
+struct PrefillPlan {
+  int n_items;
+  long long key_tiles;
+  bool split;  // some query tile has more than one chunk
+};
+PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift);
 hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s);
 bool prefill_supported(int group);
 

@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <algorithm>
+
 namespace bnr {
 namespace {
 
@@ -614,15 +616,30 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
   const int hl = lane >> 5, col = lane & 31;
-  const int h = blockIdx.x;                        // kv head (fastest: longest tiles of
-  const int qt = gridDim.y - 1 - blockIdx.y;       // every head are dispatched first)
+  const int h = blockIdx.x;  // kv head is the fastest grid axis
+  const int last_row = a.start_pos + a.n_tokens - 1;
+  // blockIdx.y -> (query tile qt, chunk ch): query tiles from the last (most
+  // keys) down, chunks of a tile consecutive, so long work is dispatched first.
+  const int csh = a.chunk_shift, ctiles = 1 << csh;
+  int qt = a.n_qtiles - 1, ch = 0, nch = 1;
+  {
+    int y = blockIdx.y;
+    for (; qt > 0; --qt) {
+      const int nk = min(a.start_pos + qt * BQ + BQ - 1, last_row) / BK + 1;
+      nch = (nk + ctiles - 1) >> csh;
+      if (y < nch) break;
+      y -= nch;
+    }
+    if (qt == 0) nch = (min(a.start_pos + BQ - 1, last_row) / BK + ctiles) >> csh;
+    ch = y;
+  }
   const int q0 = qt * BQ;
   const int qrow = min(q0 + col, a.n_tokens - 1);  // rows past the end are not stored
   const int head = h * G + g;
-  const int last_row = a.start_pos + a.n_tokens - 1;
   const int pq = a.start_pos + qrow;               // this lane's query position
   const int kmax = min(a.start_pos + q0 + BQ - 1, last_row);
-  const int nkt = kmax / BK + 1;
+  const int kt0 = ch << csh;
+  const int nkt = min(kmax / BK + 1, kt0 + ctiles);  // key tiles kt0 .. nkt-1
   const float *kc = a.k_cache + h * a.kv_stride;
   const float *vc = a.v_cache + h * a.kv_stride;
 
@@ -636,15 +653,22 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
       rv[i] = ld4(vc + off);
     }
   };
+  // V is stored column-permuted: logical dim 32*db + c sits at 4*c + db, so
+  // the four values a lane needs for one PV step are one float4.
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < F4; ++i) {
       const int f = tid + NT * i, row = f >> 5, c4 = f & 31;
       st4(&sK[buf][row][4 * c4], rk[i]);
-      st4(&sV[buf][row][4 * c4], rv[i]);
+      const int c = (4 * c4) & 31, db = (4 * c4) >> 5;
+      float *vr = &sV[buf][row][0];
+      vr[4 * c + db] = rv[i].x;
+      vr[4 * (c + 1) + db] = rv[i].y;
+      vr[4 * (c + 2) + db] = rv[i].z;
+      vr[4 * (c + 3) + db] = rv[i].w;
     }
   };
-  gload(0);
+  gload(kt0);
 
   float qf[64];
   {
@@ -664,22 +688,28 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   floatx16 O[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) O[db] = floatx16{};
-  float m = -INFINITY, l = 0.f;
+  // m starts finite: in a chunk that is not the first, a query may see no key
+  // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
+  float m = -1e30f, l = 0.f;
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
+  for (int kt = kt0; kt < nkt; ++kt) {
+    const int buf = (kt - kt0) & 1;
     if (kt + 1 < nkt) gload(kt + 1);
 
     // S^T tile: 32 keys x 32 queries.
+    // All 16 float4 of the lane's K fragment are read before the first MFMA.
     floatx16 S = floatx16{};
-    const float *krow = &sK[buf][col][64 * hl];
+    const float4 *krow = reinterpret_cast<const float4 *>(&sK[buf][col][64 * hl]);
+    float4 kf[16];
 #pragma unroll
-    for (int kk = 0; kk < 64; kk += 4) {
-      const float4 kv = *reinterpret_cast<const float4 *>(krow + kk);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[kk], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[kk + 1], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[kk + 2], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[kk + 3], S, 0, 0, 0);
+    for (int i = 0; i < 16; ++i) kf[i] = krow[i];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].x, qf[4 * i], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].y, qf[4 * i + 1], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].z, qf[4 * i + 2], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].w, qf[4 * i + 3], S, 0, 0, 0);
     }
     const int kbase = kt * BK;
     if (kbase + BK - 1 > a.start_pos + q0) {  // the tile reaches the causal diagonal
@@ -693,31 +723,86 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int r = 1; r < 16; ++r) mb = fmaxf(mb, S[r]);
     mb = fmaxf(mb, __shfl_xor(mb, 32));
-    const float mn = fmaxf(m, mb);  // finite: key 0 is visible to every query
-    const float alpha = fast_exp2(m - mn);
+    // Lazy rescaling: m is the reference the exponentials are taken against;
+    // it moves only when a query's max exceeds it by more than 8 (so every
+    // p <= 2^8).  O lives in accumulation registers, so a rescale is costly
+    // and is skipped for the whole wave when no lane needs it.  The first
+    // tile with a visible key sets m.
+    if (__ballot(mb > m + 8.0f) != 0) {
+      const float mn = fmaxf(m, mb);
+      const float alpha = fast_exp2(m - mn);
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) O[db] *= alpha;
+      m = mn;
+    }
     float p[16], ls = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = fast_exp2(S[r] - mn);
+      p[r] = fast_exp2(S[r] - m);
       ls += p[r];
     }
-    l = fmaf(l, alpha, ls);
-    m = mn;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) O[db] *= alpha;
+    l += ls;
 
-    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile.
+    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile;
+    // its four dim blocks are one float4 of the permuted V row.
+    float4 vf[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      vf[s] = *reinterpret_cast<const float4 *>(&sV[buf][8 * (s >> 2) + 4 * hl + (s & 3)][4 * col]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      const float *vrow = &sV[buf][8 * (s >> 2) + 4 * hl + (s & 3)][col];
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-        O[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * db], p[s], O[db], 0, 0, 0);
+      O[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].x, p[s], O[0], 0, 0, 0);
+      O[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].y, p[s], O[1], 0, 0, 0);
+      O[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].z, p[s], O[2], 0, 0, 0);
+      O[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].w, p[s], O[3], 0, 0, 0);
     }
     if (kt + 1 < nkt) lstore(buf ^ 1);
     __syncthreads();
   }
 
+  if (nch > 1) {
+    // Partial state of this chunk, lane-coalesced: component c (0..63 O, 64 m,
+    // 65 l) of lane `lane` of wave g at ws[((item * G + g) * 66 + c) * 64 + lane].
+    const int item0 = blockIdx.y - ch;  // first chunk of this query tile
+    float *slot = a.ws + (((long long)h * a.n_items + blockIdx.y) * G + g) * 66 * 64 + lane;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st_agent(slot + (16 * db + r) * 64, O[db][r]);
+    st_agent(slot + 64 * 64, m);
+    st_agent(slot + 65 * 64, l);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+    __syncthreads();
+    __shared__ int s_last;
+    unsigned *ctr = a.counters + ((long long)h * a.n_qtiles + qt) * kCounterStride;
+    if (tid == 0) {
+      const unsigned ticket =
+          __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = ticket == (unsigned)(nch - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Merge the other chunks into this one's registers (same lane layout).
+    for (int c = 0; c < nch; ++c) {
+      if (c == ch) continue;
+      const float *src = a.ws + (((long long)h * a.n_items + item0 + c) * G + g) * 66 * 64 + lane;
+      float ov[64];
+#pragma unroll
+      for (int i = 0; i < 64; ++i) ov[i] = ld_agent(src + i * 64);
+      const float mc = ld_agent(src + 64 * 64), lc = ld_agent(src + 65 * 64);
+      const float mn = fmaxf(m, mc);
+      const float sa = fast_exp2(m - mn), sb = fast_exp2(mc - mn);
+      l = l * sa + lc * sb;
+      m = mn;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) O[db][r] = O[db][r] * sa + ov[16 * db + r] * sb;
+    }
+  }
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
   if (q0 + col < a.n_tokens) {
     float *op = a.out + ((long long)(q0 + col) * a.n_heads + head) * D + 4 * hl;
@@ -837,9 +922,23 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
 
 bool prefill_supported(int group) { return group == 2 || group == 4 || group == 8; }
 
+PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift) {
+  const int last_row = start_pos + n_tokens - 1, nqt = (n_tokens + 31) / 32;
+  const int ctiles = 1 << chunk_shift;
+  PrefillPlan p{0, 0, false};
+  for (int qt = 0; qt < nqt; ++qt) {
+    const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
+    const int nch = (nk + ctiles - 1) >> chunk_shift;
+    p.n_items += nch;
+    p.key_tiles += nk;
+    p.split |= nch > 1;
+  }
+  return p;
+}
+
 hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s) {
   if (a.n_tokens <= 0) return hipSuccess;
-  const dim3 grid(a.n_kv, (a.n_tokens + 31) / 32);
+  const dim3 grid(a.n_kv, a.n_items);
   switch (group) {
     case 2: prefill_kernel<2><<<grid, dim3(128), 0, s>>>(a); break;
     case 4: prefill_kernel<4><<<grid, dim3(256), 0, s>>>(a); break;

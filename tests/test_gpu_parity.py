@@ -341,3 +341,39 @@ def test_dev_prefill_shapes(backend, n_heads, n_kv, n_tokens, start):
                         THETA, d_kc, d_vc, cap, out)
     np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
     assert_close(host(out), out_ref, f"prefill {n_heads}/{n_kv} n {n_tokens}")
+
+
+@pytest.mark.parametrize("shift", [0, 1, 3])
+def test_dev_prefill_key_chunks(monkeypatch, shift):
+    """Query tiles cut into key chunks of 2^shift tiles (merged by the last
+    chunk to finish), at start positions that are not tile-aligned so some
+    chunks see no key at all for their first queries; two prefills in a row
+    check that the merge tickets reset themselves."""
+    case(f"prefill key chunks shift {shift}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_CHUNK_SHIFT", str(shift))
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = 640
+        cache = oracle.KVCache(1, HKV, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(HKV, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        pre = prefill_workload(36, 45)
+        oracle_prefill(pre, cache=cache, backend=be)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(HKV, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(HKV, cap, D)))
+        start = 45
+        for n_tokens, s in ((300, 37), (129, 38)):
+            w = prefill_workload(s, n_tokens)
+            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be)
+            out = torch.zeros(n_tokens, HQ * D, device="cuda")
+            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, HQ, HKV, D,
+                               THETA, d_kc, d_vc, cap, out)
+            assert_close(host(out), out_ref, f"prefill chunks 2^{shift} n {n_tokens} start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
