@@ -82,6 +82,10 @@ struct Mirror {
   float *dk = nullptr, *dv = nullptr;
 };
 
+struct PrefillPlanEntry {
+  int n_tokens, start_pos, n_kv, shift;
+};
+
 struct DeviceGuard {
   int prev = -1;
   explicit DeviceGuard(int dev) {
@@ -141,8 +145,7 @@ struct bnr_ctx {
   // prefill planner
   int n_cu = 256;
   int pf_chunk_shift = -1;  // -1: planner decides; else key tiles per chunk = 2^shift
-  int pf_plan_key[3] = {-1, -1, -1};  // (n_tokens, start_pos, n_kv) of the last plan
-  int pf_plan_shift = 20;
+  std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> chunk shift) plans
 };
 
 namespace {
@@ -203,69 +206,138 @@ int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
   return BNR_OK;
 }
 
-// Prefill key-range chunking.  The launch's workgroups (one per CU at this
-// kernel's register use) go to the XCDs round-robin, WG i to XCD i % n_xcd,
-// and in order; a query tile with nk key tiles costs nk tile-times, plus a
-// fixed cost per workgroup (queries and first tile loaded, outputs stored),
-// plus a partial-state store when it is split and a read per merged chunk
-// for the last chunk to finish.  The planner replays that dispatch for each
-// candidate chunk size and keeps the shortest span.  Constants are in units
-// of one 32-key tile of 4 heads (measured: fixed cost ~1.8 tiles, partial
-// store ~1.8 tiles, merge read ~0.06 tiles per chunk).
+// Prefill key-range chunking.  The planner replays the launch's dispatch for
+// each candidate chunk size and keeps the shortest span.  Workgroups go to
+// the XCDs round-robin (WG i to XCD i % 8), so one XCD sees every 8th
+// workgroup of the dispatch order and the XCDs finish together; the replay
+// follows XCD 0 alone.  An XCD places a workgroup on a CU with a free slot
+// (two per CU at this kernel's register and LDS use), an idle CU first, and
+// a CU's workgroups share it: one alone runs a 32-key tile in time 1, two
+// side by side each take kShared.  A workgroup's work is its key tiles plus
+// a fixed cost (queries and first tile loaded, outputs stored), plus a
+// partial-state store when its query tile is split; the last chunk of a
+// split tile then reads the others' partials.  Constants measured on
+// MI355X (a tile of 4 heads alone on a CU takes about 4 us).
 double prefill_span(int n_tokens, int start_pos, int n_kv, int shift, int n_cu) {
-  constexpr double kFixed = 1.8, kStore = 1.8, kMerge = 0.06;
-  constexpr int kXcd = 8;
-  const int per_xcd = std::max(1, n_cu / kXcd);
-  std::vector<std::vector<double>> heaps(kXcd, std::vector<double>(per_xcd, 0.0));
-  std::vector<double> chunk_end((size_t)n_kv);
+  constexpr double kShared = 1.875, kFixed = 1.0, kStore = 1.0, kMerge = 0.25;
+  constexpr int kXcd = 8, kSlots = 2;
+  const int ncu = std::max(1, n_cu / kXcd);
+  struct Cu {
+    int n = 0;           // active workgroups
+    double rem[kSlots];  // remaining work of each
+    double tail[kSlots]; // merge work after it (split tiles)
+    double t = 0.0;      // time rem[] refers to
+    unsigned ver = 0;    // bumped whenever the finish times change
+  };
+  struct Ev {
+    double t;
+    int cu;
+    unsigned ver;
+    bool operator<(const Ev &o) const { return t > o.t; }  // min-heap
+  };
+  std::vector<Cu> cus((size_t)ncu);
+  std::vector<Ev> heap;
+  heap.reserve(256);
+  auto rate = [](int n) { return n == 1 ? 1.0 : 1.0 / kShared; };
+  auto advance = [&](Cu &c, double now) {
+    const double r = rate(c.n);
+    for (int i = 0; i < c.n; ++i) c.rem[i] -= (now - c.t) * r;
+    c.t = now;
+  };
+  auto schedule = [&](int cu) {
+    Cu &c = cus[(size_t)cu];
+    ++c.ver;
+    if (c.n == 0) return;
+    double r = c.rem[0];
+    for (int i = 1; i < c.n; ++i) r = std::min(r, c.rem[i]);
+    heap.push_back(Ev{c.t + std::max(r, 0.0) / rate(c.n), cu, c.ver});
+    std::push_heap(heap.begin(), heap.end());
+  };
+  // Free slot on the XCD: an idle CU first, else one running a single workgroup.
+  auto pick = [&]() {
+    int best = -1;
+    for (int i = 0; i < ncu; ++i) {
+      if (cus[(size_t)i].n == 0) return i;
+      if (best < 0 && cus[(size_t)i].n < kSlots) best = i;
+    }
+    return best;
+  };
+
   const int last_row = start_pos + n_tokens - 1, nqt = (n_tokens + 31) / 32;
   const int ctiles = 1 << std::min(shift, 20);
-  auto later = [](double a, double b) { return a > b; };  // min-heaps
-  double span = 0.0, t_last = 0.0;
+  double now = 0.0, span = 0.0;
   long long wg = 0;
   for (int qt = nqt - 1; qt >= 0; --qt) {
     const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
     const int nch = (nk + ctiles - 1) / ctiles;
-    std::fill(chunk_end.begin(), chunk_end.end(), 0.0);
     for (int ch = 0; ch < nch; ++ch) {
       const int t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
       for (int h = 0; h < n_kv; ++h, ++wg) {
-        std::vector<double> &hp = heaps[(size_t)(wg % kXcd)];
-        std::pop_heap(hp.begin(), hp.end(), later);
-        const double start = std::max(hp.back(), t_last);
-        t_last = start;
-        const double end = start + kFixed + t + (nch > 1 ? kStore : 0.0);
-        hp.back() = end;
-        std::push_heap(hp.begin(), hp.end(), later);
-        chunk_end[(size_t)h] = std::max(chunk_end[(size_t)h], end);
-        span = std::max(span, end);
+        if (wg % kXcd != 0) continue;
+        int cu;
+        while ((cu = pick()) < 0) {  // wait for a slot: run to the next finish
+          std::pop_heap(heap.begin(), heap.end());
+          const Ev ev = heap.back();
+          heap.pop_back();
+          Cu &c = cus[(size_t)ev.cu];
+          if (ev.ver != c.ver) continue;
+          now = ev.t;
+          advance(c, now);
+          for (int i = 0; i < c.n;) {
+            if (c.rem[i] <= 1e-9) {
+              span = std::max(span, now + c.tail[i]);
+              c.rem[i] = c.rem[c.n - 1];
+              c.tail[i] = c.tail[c.n - 1];
+              --c.n;
+            } else {
+              ++i;
+            }
+          }
+          schedule(ev.cu);
+        }
+        Cu &c = cus[(size_t)cu];
+        advance(c, now);
+        c.rem[c.n] = kFixed + t + (nch > 1 ? kStore : 0.0);
+        c.tail[c.n] = nch > 1 ? (nch - 1) * kMerge : 0.0;
+        ++c.n;
+        schedule(cu);
       }
     }
-    if (nch > 1)
-      for (int h = 0; h < n_kv; ++h)
-        span = std::max(span, chunk_end[(size_t)h] + (nch - 1) * kMerge);
+  }
+  for (Cu &c : cus) {  // drain
+    const double r = rate(c.n);
+    for (int i = 0; i < c.n; ++i) {
+      // the shorter of two shared workgroups ends first, the other then runs alone
+      double end;
+      if (c.n == 2) {
+        const double a = std::min(c.rem[0], c.rem[1]), b = std::max(c.rem[0], c.rem[1]);
+        end = c.t + (c.rem[i] == a ? a / r : a / r + (b - a));
+      } else {
+        end = c.t + c.rem[i] / r;
+      }
+      span = std::max(span, end + c.tail[i]);
+    }
   }
   return span;
 }
 
+// Chunk shift for a prefill shape (20: no split); the last 16 shapes are
+// remembered, a new one costs a few replays (tens to hundreds of us).
 int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
-  if (c->pf_plan_key[0] == n_tokens && c->pf_plan_key[1] == start_pos &&
-      c->pf_plan_key[2] == n_kv)
-    return c->pf_plan_shift;
+  for (const PrefillPlanEntry &e : c->pf_plans)
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) return e.shift;
   int best = 20;
   double best_span = prefill_span(n_tokens, start_pos, n_kv, 20, c->n_cu);
   for (int shift = 2; shift <= 6; ++shift) {
-    if (prefill_plan(n_tokens, start_pos, shift).n_items * (long long)n_kv > 16384) continue;
+    if (prefill_plan(n_tokens, start_pos, shift).n_items * (long long)n_kv > 8192) continue;
     const double span = prefill_span(n_tokens, start_pos, n_kv, shift, c->n_cu);
     if (span < best_span * 0.99) {
       best_span = span;
       best = shift;
     }
   }
-  c->pf_plan_key[0] = n_tokens;
-  c->pf_plan_key[1] = start_pos;
-  c->pf_plan_key[2] = n_kv;
-  c->pf_plan_shift = best;
+  if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
+  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, best});
   return best;
 }
 

@@ -591,30 +591,63 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 // Causal flash prefill on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
 //
 // Workgroup = one kv head's G query heads (one wave each) x 32 queries; the
-// G waves share every 32-key K/V tile, staged in LDS (double buffered, rows
-// padded to 132 floats so that the 32 lanes of a half-wave hit distinct
-// banks).  Each wave computes S^T = K Q^T (32 keys x 32 queries), so the
-// accumulator layout of S^T is exactly the B-operand layout P^T needs for
-// O^T = V^T P^T: no transposes, no LDS round trip for P.
+// G waves share every 32-key K/V tile.  Tiles go from HBM straight into LDS
+// (global_load_lds, 16 bytes per lane, no staging registers), double
+// buffered in four separate LDS arrays so that the compiler can tell a read
+// of the current tile from the copy of the next one still in flight.  The
+// register budget (at most 256 per lane) lets two workgroups share a CU:
+// one's softmax, LDS reads and start-up run under the other's MFMAs.
+//
+// Each wave computes S^T = K Q^T (32 keys x 32 queries), so the accumulator
+// layout of S^T is exactly the B-operand layout P^T needs for O^T = V^T P^T:
+// no transposes, no LDS round trip for P.
 //
 // Lane l of a wave: col = l % 32 is its query, hl = l / 32 its half.  Q
 // fragment: dims 64*hl .. 64*hl+63 of that query (registers, prescaled by
 // log2(e)/sqrt(d)).  MFMA step kk (0..63) uses dim 64*hl + kk for the lane's
-// k-slot, so K rows are read from LDS as contiguous float4s.  Accumulator
-// register r of a 32x32 tile holds row 8*(r/4) + 4*hl + r%4.  Online softmax
-// per query: a key tile's max and sum are the lane's 16 values plus its
-// partner lane l^32.  Query tiles with the most keys are dispatched first.
+// k-slot, so K rows are read from LDS as float4s; K rows are stored with
+// their 16-byte chunks XOR-swizzled by (row % 16) so that the 32 rows read
+// at one step fall in distinct banks.  Accumulator register r of a 32x32
+// tile holds row 8*(r/4) + 4*hl + r%4.  In O^T, row i of dim block db is
+// head dim 4*i + db, so the four values a lane needs for one PV step are
+// the float4 at dims 4*col of one V row, unpermuted.  Online softmax per
+// query: a key tile's max and sum are the lane's 16 values plus its partner
+// lane l^32.
+//
+// Long query tiles are cut into key chunks of 2^chunk_shift tiles (separate
+// workgroups); the last chunk of a tile to finish merges the others' partial
+// states.  Work items are dispatched longest query tile first.
 // ---------------------------------------------------------------------------
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
 
+// 16 bytes per lane from global memory straight into LDS: lane i of the wave
+// writes bytes [16 i, 16 i + 16) after `lds`, which must be wave-uniform.
+__device__ __forceinline__ void dma16(const float *g, float *lds) {
+  __builtin_amdgcn_global_load_lds((global_void_t *)g, (lds_void_t *)lds, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Two waves per SIMD: at most 256 registers per lane.  (G = 2 reaches only
+// one: two of its workgroups fill LDS.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <int G>
-__global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
-  constexpr int D = kHeadDim, BQ = 32, BK = 32, KP = D + 4, NT = 64 * G;
-  constexpr int F4 = BK * D / 4 / NT;  // float4 of K (and of V) per lane per tile
-  __shared__ float sK[2][BK][KP];
-  __shared__ float sV[2][BK][KP];
+__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_kernel(PrefillArgs a) {
+  constexpr int D = kHeadDim, BQ = 32, BK = 32;
+  constexpr int TILE = BK * D;            // floats per K (or V) tile
+  constexpr int NI = TILE / 4 / (64 * G); // 1 KB copies per wave per tile
+  __shared__ __attribute__((aligned(16))) float sK0[TILE];
+  __shared__ __attribute__((aligned(16))) float sK1[TILE];
+  __shared__ __attribute__((aligned(16))) float sV0[TILE];
+  __shared__ __attribute__((aligned(16))) float sV1[TILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave;
   const int hl = lane >> 5, col = lane & 31;
   const int h = blockIdx.x;  // kv head is the fastest grid axis
   const int last_row = a.start_pos + a.n_tokens - 1;
@@ -643,32 +676,20 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   const float *kc = a.k_cache + h * a.kv_stride;
   const float *vc = a.v_cache + h * a.kv_stride;
 
-  float4 rk[F4], rv[F4];
-  auto gload = [&](int kt) {
+  // Copy of key tile kt: copy j of wave w fills rows 2J, 2J+1 (J = w*NI + j);
+  // lane l takes row 2J + l/32, LDS chunk l%32.  Rows past the last cached
+  // one repeat it (their keys are masked for every query).
+  auto copy_tile = [&](int kt, float *dk, float *dv) {
 #pragma unroll
-    for (int i = 0; i < F4; ++i) {
-      const int f = tid + NT * i, row = f >> 5, c4 = f & 31;
-      const long long off = (long long)min(kt * BK + row, last_row) * D + 4 * c4;
-      rk[i] = ld4(kc + off);
-      rv[i] = ld4(vc + off);
+    for (int j = 0; j < NI; ++j) {
+      const int J = wave * NI + j;
+      const int r = 2 * J + hl, p = col;
+      const long long grow = (long long)min(kt * BK + r, last_row) * D;
+      dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
+      dma16(vc + grow + 4 * p, dv + J * 256);
     }
   };
-  // V is stored column-permuted: logical dim 32*db + c sits at 4*c + db, so
-  // the four values a lane needs for one PV step are one float4.
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < F4; ++i) {
-      const int f = tid + NT * i, row = f >> 5, c4 = f & 31;
-      st4(&sK[buf][row][4 * c4], rk[i]);
-      const int c = (4 * c4) & 31, db = (4 * c4) >> 5;
-      float *vr = &sV[buf][row][0];
-      vr[4 * c + db] = rv[i].x;
-      vr[4 * (c + 1) + db] = rv[i].y;
-      vr[4 * (c + 2) + db] = rv[i].z;
-      vr[4 * (c + 3) + db] = rv[i].w;
-    }
-  };
-  gload(kt0);
+  copy_tile(kt0, sK0, sV0);
 
   float qf[64];
   {
@@ -682,7 +703,7 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
       qf[4 * i + 3] = v.w * a.scale_log2;
     }
   }
-  lstore(0);
+  wait_vmem();
   __syncthreads();
 
   floatx16 O[4];
@@ -692,24 +713,20 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
   // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
   float m = -1e30f, l = 0.f;
 
-  for (int kt = kt0; kt < nkt; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    if (kt + 1 < nkt) gload(kt + 1);
+  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv) {
+    if (kt + 1 < nkt) copy_tile(kt + 1, nk, nv);
 
     // S^T tile: 32 keys x 32 queries.
-    // All 16 float4 of the lane's K fragment are read before the first MFMA.
     floatx16 S = floatx16{};
-    const float4 *krow = reinterpret_cast<const float4 *>(&sK[buf][col][64 * hl]);
-    float4 kf[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) kf[i] = krow[i];
-    __builtin_amdgcn_sched_barrier(0);
+    const float *krow = dk + col * D + 64 * hl;
+    const int sw = col & 15;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].x, qf[4 * i], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].y, qf[4 * i + 1], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].z, qf[4 * i + 2], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i].w, qf[4 * i + 3], S, 0, 0, 0);
+      const float4 kv = ld4(krow + 4 * (i ^ sw));
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * i], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * i + 1], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * i + 2], S, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
     }
     const int kbase = kt * BK;
     if (kbase + BK - 1 > a.start_pos + q0) {  // the tile reaches the causal diagonal
@@ -744,22 +761,23 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
     }
     l += ls;
 
-    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile;
-    // its four dim blocks are one float4 of the permuted V row.
-    float4 vf[16];
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-      vf[s] = *reinterpret_cast<const float4 *>(&sV[buf][8 * (s >> 2) + 4 * hl + (s & 3)][4 * col]);
-    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile.
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
-      O[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].x, p[s], O[0], 0, 0, 0);
-      O[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].y, p[s], O[1], 0, 0, 0);
-      O[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].z, p[s], O[2], 0, 0, 0);
-      O[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[s].w, p[s], O[3], 0, 0, 0);
+      const float4 vv = ld4(dv + (8 * (s >> 2) + 4 * hl + (s & 3)) * D + 4 * col);
+      O[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, p[s], O[0], 0, 0, 0);
+      O[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, p[s], O[1], 0, 0, 0);
+      O[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[s], O[2], 0, 0, 0);
+      O[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[s], O[3], 0, 0, 0);
     }
-    if (kt + 1 < nkt) lstore(buf ^ 1);
+    wait_vmem();  // this wave's copies of the next tile have landed
     __syncthreads();
+  };
+  for (int kt = kt0;;) {
+    step(kt, sK0, sV0, sK1, sV1);
+    if (++kt >= nkt) break;
+    step(kt, sK1, sV1, sK0, sV0);
+    if (++kt >= nkt) break;
   }
 
   if (nch > 1) {
@@ -803,18 +821,17 @@ __global__ __launch_bounds__(64 * G) void prefill_kernel(PrefillArgs a) {
         for (int r = 0; r < 16; ++r) O[db][r] = O[db][r] * sa + ov[16 * db + r] * sb;
     }
   }
+  // Lane (col, hl) holds, for r = 4*rq + r3, dims 32*rq + 16*hl + 4*r3 + db.
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
   if (q0 + col < a.n_tokens) {
-    float *op = a.out + ((long long)(q0 + col) * a.n_heads + head) * D + 4 * hl;
+    float *op = a.out + ((long long)(q0 + col) * a.n_heads + head) * D + 16 * hl;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq)
-        st4(op + 32 * db + 8 * rq,
-            make_float4(O[db][4 * rq] * inv, O[db][4 * rq + 1] * inv, O[db][4 * rq + 2] * inv,
-                        O[db][4 * rq + 3] * inv));
+    for (int r = 0; r < 16; ++r)
+      st4(op + 32 * (r >> 2) + 4 * (r & 3),
+          make_float4(O[0][r] * inv, O[1][r] * inv, O[2][r] * inv, O[3][r] * inv));
   }
 }
+#pragma clang diagnostic pop
 
 // ---------------------------------------------------------------------------
 // Generic decode attention (any head_dim, any group size).  Same three
