@@ -628,6 +628,43 @@ __device__ __forceinline__ void dma16(const float *g, float *lds) {
   __builtin_amdgcn_global_load_lds((global_void_t *)g, (lds_void_t *)lds, 16, 0, 0);
 }
 
+// Sum over x = 1..m of ceil(x / 2^sh).
+__device__ __forceinline__ long long ceil_sum(long long m, int sh) {
+  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
+  return ((q * (q + 1) >> 1) << sh) + r * (q + 1);
+}
+
+// Work item y of a prefill launch -> (query tile qt, chunk ch of nch).  Items
+// run over query tiles from the last down, chunks of a tile consecutive.  The
+// last tile may be short; every other tile qt has qt + A key tiles with
+// A = ceil((start_pos + 1) / 32) (its last query sits at start_pos + 32 qt + 31),
+// so the items of tiles q .. nqt-2 are a difference of two ceil sums and the
+// tile of item y is found by binary search.
+__device__ __forceinline__ void prefill_item(int y, int nqt, int start_pos, int last_row, int sh,
+                                             int &qt, int &ch, int &nch) {
+  const int ct = 1 << sh;
+  const int nch_last = (last_row / 32 + 1 + ct - 1) >> sh;
+  if (y < nch_last) {
+    qt = nqt - 1;
+    ch = y;
+    nch = nch_last;
+    return;
+  }
+  const long long yy = y - nch_last;
+  const int A = (start_pos + 31) / 32 + 1;
+  const long long top = ceil_sum(nqt - 2 + A, sh);
+  // items of tiles q .. nqt-2: top - ceil_sum(q - 1 + A); largest q with more than yy
+  int lo = 0, hi = nqt - 2;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (top - ceil_sum(mid - 1 + A, sh) > yy) lo = mid;
+    else hi = mid - 1;
+  }
+  qt = lo;
+  ch = (int)(yy - (top - ceil_sum(lo + A, sh)));
+  nch = (lo + A + ct - 1) >> sh;
+}
+
 // s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -654,18 +691,8 @@ void prefill_kernel(PrefillArgs a) {
   // blockIdx.y -> (query tile qt, chunk ch): query tiles from the last (most
   // keys) down, chunks of a tile consecutive, so long work is dispatched first.
   const int csh = a.chunk_shift, ctiles = 1 << csh;
-  int qt = a.n_qtiles - 1, ch = 0, nch = 1;
-  {
-    int y = blockIdx.y;
-    for (; qt > 0; --qt) {
-      const int nk = min(a.start_pos + qt * BQ + BQ - 1, last_row) / BK + 1;
-      nch = (nk + ctiles - 1) >> csh;
-      if (y < nch) break;
-      y -= nch;
-    }
-    if (qt == 0) nch = (min(a.start_pos + BQ - 1, last_row) / BK + ctiles) >> csh;
-    ch = y;
-  }
+  int qt, ch, nch;
+  prefill_item(blockIdx.y, a.n_qtiles, a.start_pos, last_row, csh, qt, ch, nch);
   const int q0 = qt * BQ;
   const int qrow = min(q0 + col, a.n_tokens - 1);  // rows past the end are not stored
   const int head = h * G + g;
