@@ -20,6 +20,7 @@ BNR_INVALID_SHAPE = 1
 BNR_INVALID_CONFIG = 2
 BNR_BACKEND_ERROR = 3
 BNR_UNSUPPORTED_DEVICE = 4
+BNR_QUANTIZATION_ERROR = 5
 
 BNR_MIRROR_INCREMENTAL = 0
 BNR_MIRROR_FULL = 1
@@ -47,11 +48,16 @@ class UnsupportedDevice(BitNetError):
     kind = BNR_UNSUPPORTED_DEVICE
 
 
+class QuantizationError(BitNetError):
+    kind = BNR_QUANTIZATION_ERROR
+
+
 ERRORS = {
     BNR_INVALID_SHAPE: InvalidShape,
     BNR_INVALID_CONFIG: InvalidConfig,
     BNR_BACKEND_ERROR: BackendError,
     BNR_UNSUPPORTED_DEVICE: UnsupportedDevice,
+    BNR_QUANTIZATION_ERROR: QuantizationError,
 }
 
 
@@ -92,6 +98,10 @@ SIGNATURES = {
                                              _sz, _vp]),
     "bnr_dev_prefill": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _c.c_float, _vp,
                                    _vp, _sz, _vp, _vp]),
+    "bnr_ternary_gemv_preq": (_c.c_int, [_vp, _vp, _sz, _c.c_float, _vp, _sz, _c.c_float, _f,
+                                         _sz, _sz, _sz]),
+    "bnr_dev_ternary_gemv_preq": (_c.c_int, [_vp, _vp, _c.c_float, _vp, _c.c_float, _vp, _sz,
+                                             _sz, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
 }
 

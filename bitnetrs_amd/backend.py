@@ -19,10 +19,11 @@ import numpy as np
 
 from . import _lib
 from ._lib import (BNR_MIRROR_FULL, BNR_MIRROR_INCREMENTAL, BackendError, BitNetError,
-                   InvalidConfig, InvalidShape, UnsupportedDevice)
+                   InvalidConfig, InvalidShape, QuantizationError, UnsupportedDevice)
 
 __all__ = ["HipBackend", "DeviceKVCache", "BitNetError", "InvalidShape", "InvalidConfig",
-           "BackendError", "UnsupportedDevice", "BNR_MIRROR_FULL", "BNR_MIRROR_INCREMENTAL"]
+           "BackendError", "UnsupportedDevice", "QuantizationError", "BNR_MIRROR_FULL",
+           "BNR_MIRROR_INCREMENTAL"]
 
 _fp = ctypes.POINTER(ctypes.c_float)
 
@@ -33,16 +34,23 @@ def _host(a: np.ndarray, name: str):
     return a.ctypes.data_as(_fp) if a.size else _fp()
 
 
-def _dev(t, name: str, allow_none: bool = False):
+def _host_bytes(a: np.ndarray, dtype, name: str):
+    if not isinstance(a, np.ndarray) or a.dtype != dtype or not a.flags.c_contiguous:
+        raise TypeError(f"{name} must be a C-contiguous {np.dtype(dtype).name} numpy array")
+    return ctypes.c_void_p(a.ctypes.data if a.size else 0)
+
+
+def _dev(t, name: str, allow_none: bool = False, dtype=None):
     if t is None:
         if allow_none:
             return None
         raise TypeError(f"{name} is required")
     import torch
 
-    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32
+    dtype = dtype or torch.float32
+    if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == dtype
             and t.is_contiguous()):
-        raise TypeError(f"{name} must be a contiguous float32 CUDA tensor")
+        raise TypeError(f"{name} must be a contiguous {dtype} CUDA tensor")
     return ctypes.c_void_p(t.data_ptr())
 
 
@@ -104,6 +112,17 @@ class HipBackend:
             _host(v_cache, "v_cache"), v_cache.size, _host(output, "output"), output.size,
             n_heads, n_kv_heads, head_dim, cur_pos))
 
+    def ternary_gemv_preq(self, weight_packed: np.ndarray, weight_scale: float,
+                          activation_q: np.ndarray, act_absmax: float, output: np.ndarray,
+                          out_features: int, in_features: int) -> None:
+        """Backend::ternary_gemv_preq (bitnet-core/src/backend/mod.rs:459-468): packed
+        2-bit weights (uint8, mirrored in HBM on first use), int8 activations,
+        output overwritten."""
+        _lib.check(self._L.bnr_ternary_gemv_preq(
+            self._h, _host_bytes(weight_packed, np.uint8, "weight_packed"), weight_packed.size,
+            weight_scale, _host_bytes(activation_q, np.int8, "activation_q"), activation_q.size,
+            act_absmax, _host(output, "output"), output.size, out_features, in_features))
+
     def set_mirror_mode(self, mode: int) -> None:
         _lib.check(self._L.bnr_set_mirror_mode(self._h, mode))
 
@@ -154,6 +173,15 @@ class HipBackend:
             self._h, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_tokens, start_pos, n_heads,
             n_kv_heads, head_dim, theta, _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
             _dev(out, "out"), _stream(stream)))
+
+    def dev_ternary_gemv_preq(self, weight_packed, weight_scale, activation_q, act_absmax, output,
+                              out_features, in_features, stream=None) -> None:
+        import torch
+
+        _lib.check(self._L.bnr_dev_ternary_gemv_preq(
+            self._h, _dev(weight_packed, "weight_packed", dtype=torch.uint8), weight_scale,
+            _dev(activation_q, "activation_q", dtype=torch.int8), act_absmax,
+            _dev(output, "output"), out_features, in_features, _stream(stream)))
 
     def dev_synchronize(self, stream=None) -> None:
         _lib.check(self._L.bnr_dev_synchronize(self._h, _stream(stream)))

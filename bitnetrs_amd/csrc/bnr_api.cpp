@@ -58,6 +58,42 @@ static int err_backend(const std::string &msg) {
   return BNR_BACKEND_ERROR;
 }
 
+static int err_quant(const std::string &msg) {
+  g_err = "quantization error: " + msg;
+  return BNR_QUANTIZATION_ERROR;
+}
+
+// Rust's Display of an f32: the shortest decimal that reads back to the same
+// value, written positionally ("0.5", "-3", "0.0000001", "NaN", "inf").
+static std::string rust_f32(float x) {
+  if (std::isnan(x)) return "NaN";
+  if (std::isinf(x)) return x < 0 ? "-inf" : "inf";
+  if (x == 0.0f) return std::signbit(x) ? "-0" : "0";
+  char e[64];
+  int p = 1;
+  for (; p <= 9; ++p) {
+    snprintf(e, sizeof e, "%.*e", p - 1, (double)x);
+    if ((float)strtod(e, nullptr) == x) break;
+  }
+  std::string digits;
+  const bool neg = e[0] == '-';
+  const char *q = e + (neg ? 1 : 0);
+  for (; *q && *q != 'e'; ++q)
+    if (*q != '.') digits += *q;
+  const int ex = atoi(q + 1);
+  while (digits.size() > 1 && digits.back() == '0') digits.pop_back();
+  const int nd = (int)digits.size();
+  std::string out = neg ? "-" : "";
+  if (ex >= nd - 1) {
+    out += digits + std::string((size_t)(ex - (nd - 1)), '0');
+  } else if (ex >= 0) {
+    out += digits.substr(0, (size_t)ex + 1) + "." + digits.substr((size_t)ex + 1);
+  } else {
+    out += "0." + std::string((size_t)(-ex - 1), '0') + digits;
+  }
+  return out;
+}
+
 static int err_hip(hipError_t e, const char *what) {
   return err_backend(std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -81,6 +117,26 @@ struct Mirror {
   size_t synced = 0;  // rows 0..synced-1 match the host
   float *dk = nullptr, *dv = nullptr;
 };
+
+// HBM copy of one host ternary weight matrix, for bnr_ternary_gemv_preq.
+// The fingerprint (64 bytes sampled across the buffer) catches a different
+// matrix placed at the same address with the same length, which a freed and
+// reallocated host buffer can be; rewriting weights in place still needs
+// bnr_mirror_invalidate.
+constexpr int kFingerprint = 64;
+struct WeightMirror {
+  const uint8_t *host = nullptr;
+  size_t len = 0;
+  uint8_t *dev = nullptr;
+  uint8_t print[kFingerprint] = {};
+};
+
+void fingerprint(const uint8_t *p, size_t len, uint8_t *out) {
+  for (int i = 0; i < kFingerprint; ++i)
+    out[i] = p[len > 1 ? (size_t)i * (len - 1) / (kFingerprint - 1) : 0];
+}
+
+constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
   int n_tokens, start_pos, n_kv, shift;
@@ -134,6 +190,9 @@ struct bnr_ctx {
 
   // mirrors, most recently used first
   std::list<Mirror> mirrors;
+  std::list<WeightMirror> weight_mirrors;
+  uint8_t *d_bytes = nullptr;  // int8 activation staging
+  size_t d_bytes_n = 0;
   int mirror_mode = BNR_MIRROR_INCREMENTAL;
 
   // decode planner
@@ -347,7 +406,7 @@ int build_table(bnr_ctx *c, size_t max_seq, size_t head_dim, float theta) {
   if (head_dim == 0 || head_dim % 2 != 0)
     return err_config(fmt("head_dim must be even and > 0, got %zu", head_dim));
   if (!(theta > 0.0f) || !std::isfinite(theta))
-    return err_config(fmt("theta must be finite and > 0, got %g", (double)theta));
+    return err_config("theta must be finite and > 0, got " + rust_f32(theta));
   const size_t half = head_dim / 2, n = max_seq * half;
   std::vector<float> hc(n), hs(n);
   for (size_t pos = 0; pos < max_seq; ++pos) {
@@ -517,7 +576,7 @@ Mirror *find_mirror(bnr_ctx *c, const float *hk, size_t k_len, const float *hv, 
 // ---------------------------------------------------------------------------
 extern "C" const char *bnr_last_error(void) { return g_err.c_str(); }
 
-extern "C" uint32_t bnr_abi_version(void) { return (1u << 16) | 0u; }
+extern "C" uint32_t bnr_abi_version(void) { return (1u << 16) | 1u; }
 
 extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (!out) return err_backend("bnr_create: out is NULL");
@@ -567,6 +626,9 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     DeviceGuard dg(c->device);
     (void)hipDeviceSynchronize();
     for (auto &m : c->mirrors) free_mirror(m);
+    for (auto &m : c->weight_mirrors)
+      if (m.dev) (void)hipFree(m.dev);
+    if (c->d_bytes) (void)hipFree(c->d_bytes);
     float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out, c->pf_ws};
     for (float *p : bufs)
       if (p) (void)hipFree(p);
@@ -744,6 +806,137 @@ extern "C" int bnr_mirror_invalidate(bnr_ctx *c) {
   if (!c) return err_backend("context is NULL");
   std::lock_guard<std::mutex> lk(c->mu);
   for (auto &m : c->mirrors) m.synced = 0;
+  if (!c->weight_mirrors.empty()) {
+    DeviceGuard dg(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    for (auto &m : c->weight_mirrors)
+      if (m.dev) (void)hipFree(m.dev);
+    c->weight_mirrors.clear();
+  }
+  return set_ok();
+}
+
+// ---------------------------------------------------------------------------
+// W2A8 ternary GEMV
+// ---------------------------------------------------------------------------
+namespace {
+
+// Checks of gemv::ternary_gemv_quantised (bitnet-cpu/src/gemv.rs:384-420),
+// in its order, for the lengths that are given (SIZE_MAX: not checked).
+int check_gemv(size_t weight_len, float weight_scale, size_t act_len, float act_absmax,
+               size_t out_len, size_t out_features, size_t in_features) {
+  const size_t packed_cols = (in_features + 3) / 4;
+  if (packed_cols != 0 && out_features > SIZE_MAX / packed_cols)
+    return err_shape("weight size fits usize", "overflow");
+  const size_t expected = out_features * packed_cols;
+  if (weight_len != SIZE_MAX && weight_len != expected)
+    return err_shape(fmt("weight_packed.len() == %zu * ceil(%zu/4) = %zu", out_features,
+                         in_features, expected),
+                     fmt("weight_packed.len() == %zu", weight_len));
+  if (act_len != SIZE_MAX && act_len != in_features)
+    return err_shape(fmt("activation.len() == %zu", in_features),
+                     fmt("activation.len() == %zu", act_len));
+  if (out_len != SIZE_MAX && out_len != out_features)
+    return err_shape(fmt("output.len() == %zu", out_features), fmt("output.len() == %zu", out_len));
+  if (weight_scale <= 0.0f || !std::isfinite(weight_scale))
+    return err_quant("weight_scale must be finite > 0, got " + rust_f32(weight_scale));
+  if (act_absmax <= 0.0f || !std::isfinite(act_absmax))
+    return err_quant("act_scale must be finite > 0, got " + rust_f32(act_absmax));
+  if (out_features > (size_t)INT32_MAX || in_features > (size_t)INT32_MAX)
+    return err_backend("ternary_gemv_preq: dimensions beyond 2^31 are not supported");
+  return BNR_OK;
+}
+
+int run_gemv(const uint8_t *w, float weight_scale, const int8_t *act, float act_absmax, float *out,
+             size_t out_features, size_t in_features, hipStream_t s) {
+  TernaryGemvArgs a{};
+  a.weight = w;
+  a.act = act;
+  a.out = out;
+  a.packed_cols = (long long)((in_features + 3) / 4);
+  a.out_features = (int)out_features;
+  a.in_features = (int)in_features;
+  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), f32, left to right
+  volatile float ws_as = weight_scale * act_absmax;
+  a.scale = ws_as / 127.0f;
+  const bool vec = a.packed_cols % 16 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)act % 16) == 0;
+  HIP_TRY(launch_ternary_gemv(a, vec, s), "ternary_gemv launch");
+  return BNR_OK;
+}
+
+}  // namespace
+
+extern "C" int bnr_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed, size_t weight_len,
+                                     float weight_scale, const int8_t *activation_q,
+                                     size_t act_len, float act_absmax, float *output,
+                                     size_t out_len, size_t out_features, size_t in_features) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_gemv(weight_len, weight_scale, act_len, act_absmax, out_len, out_features,
+                      in_features);
+  if (st) return st;
+  if (out_features == 0) return set_ok();
+  if ((weight_len && !weight_packed) || (act_len && !activation_q) || !output)
+    return err_backend("ternary_gemv_preq: NULL slice");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  const uint8_t *dw = nullptr;
+  if (weight_len) {
+    uint8_t print[kFingerprint];
+    fingerprint(weight_packed, weight_len, print);
+    auto it = c->weight_mirrors.begin();
+    for (; it != c->weight_mirrors.end(); ++it)
+      if (it->host == weight_packed && it->len == weight_len) break;
+    if (it != c->weight_mirrors.end() && std::memcmp(it->print, print, kFingerprint) != 0) {
+      (void)hipStreamSynchronize(c->stream);  // a different matrix at the same address
+      (void)hipFree(it->dev);
+      c->weight_mirrors.erase(it);
+      it = c->weight_mirrors.end();
+    }
+    if (it != c->weight_mirrors.end()) {
+      c->weight_mirrors.splice(c->weight_mirrors.begin(), c->weight_mirrors, it);
+    } else {
+      if (c->weight_mirrors.size() >= kMaxWeightMirrors) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->weight_mirrors.back().dev);
+        c->weight_mirrors.pop_back();
+      }
+      WeightMirror m;
+      m.host = weight_packed;
+      m.len = weight_len;
+      std::memcpy(m.print, print, kFingerprint);
+      HIP_TRY(hipMalloc((void **)&m.dev, weight_len), "weight mirror alloc");
+      hipError_t e = hipMemcpyAsync(m.dev, weight_packed, weight_len, hipMemcpyHostToDevice,
+                                    c->stream);
+      if (e != hipSuccess) {
+        (void)hipFree(m.dev);
+        return err_hip(e, "weight upload");
+      }
+      c->weight_mirrors.push_front(m);
+    }
+    dw = c->weight_mirrors.front().dev;
+  }
+  if (c->d_bytes_n < std::max<size_t>(in_features, 16)) {
+    if (c->d_bytes) {
+      (void)hipStreamSynchronize(c->stream);
+      (void)hipFree(c->d_bytes);
+      c->d_bytes = nullptr;
+      c->d_bytes_n = 0;
+    }
+    const size_t want = std::max<size_t>(in_features, 4096);
+    HIP_TRY(hipMalloc((void **)&c->d_bytes, want), "staging alloc");
+    c->d_bytes_n = want;
+  }
+  st = ensure_buf(&c->d_out, &c->d_out_n, out_features, "staging alloc");
+  if (st) return st;
+  if (in_features)
+    HIP_TRY(hipMemcpyAsync(c->d_bytes, activation_q, in_features, hipMemcpyHostToDevice, c->stream),
+            "upload activation");
+  st = run_gemv(dw, weight_scale, (const int8_t *)c->d_bytes, act_absmax, c->d_out, out_features,
+                in_features, c->stream);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(output, c->d_out, out_features * 4, hipMemcpyDeviceToHost, c->stream),
+          "download output");
+  HIP_TRY(hipStreamSynchronize(c->stream), "ternary_gemv_preq");
   return set_ok();
 }
 
@@ -765,7 +958,7 @@ int check_rope(size_t head_dim, float theta) {
   if (head_dim == 0 || head_dim % 2 != 0)
     return err_config(fmt("head_dim must be even and > 0, got %zu", head_dim));
   if (!(theta > 0.0f) || !std::isfinite(theta))
-    return err_config(fmt("theta must be finite and > 0, got %g", (double)theta));
+    return err_config("theta must be finite and > 0, got " + rust_f32(theta));
   return BNR_OK;
 }
 
@@ -1046,6 +1239,24 @@ extern "C" int bnr_dev_prefill(bnr_ctx *c, float *q, float *k, const float *v, s
   if (st) return st;
   return bnr_dev_prefill_attention(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
                                    n_kv_heads, head_dim, stream);
+}
+
+extern "C" int bnr_dev_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed,
+                                         float weight_scale, const int8_t *activation_q,
+                                         float act_absmax, float *output, size_t out_features,
+                                         size_t in_features, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_gemv(SIZE_MAX, weight_scale, SIZE_MAX, act_absmax, SIZE_MAX, out_features,
+                      in_features);
+  if (st) return st;
+  if (out_features == 0) return set_ok();
+  if ((in_features && (!weight_packed || !activation_q)) || !output)
+    return err_backend("ternary_gemv_preq: NULL pointer");
+  DeviceGuard dg(c->device);
+  st = run_gemv(weight_packed, weight_scale, activation_q, act_absmax, output, out_features,
+                in_features, (hipStream_t)stream);
+  if (st) return st;
+  return set_ok();
 }
 
 extern "C" int bnr_dev_synchronize(bnr_ctx *c, void *stream) {

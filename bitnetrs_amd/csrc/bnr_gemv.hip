@@ -1,0 +1,146 @@
+// bnr_gemv.hip -- W2A8 ternary GEMV for gfx950 (Backend::ternary_gemv_preq).
+//
+// out[i] = (float)(sum_j W[i][j] * a[j]) * scale, with W in {-1, 0, +1}
+// stored 2 bits per weight (row-aligned, ceil(K/4) bytes per row; code
+// 0b00 -> +1, 0b01 -> 0, 0b10 -> -1, 0b11 -> 0, weight 4b+p at bits 2p of
+// byte b) and a[] int8.  The integer sum is exact, so the result is
+// bit-identical to the reference's (bitnet-cpu/src/gemv.rs:368-430).
+//
+// Memory-bound: each packed weight byte is read once.  A workgroup owns 16
+// rows, 16 lanes per row; a lane takes the row's 16-byte pieces j, j+16, ...
+// (64 weights each).  The K activations are staged in LDS once per workgroup
+// and pass (4096 per pass), transposed so that one v_dot4_i32_i8 pairs four
+// decoded weights with their activations without unpacking the 2-bit codes
+// into bytes.
+#include "bnr_internal.h"
+
+#include <hip/hip_runtime.h>
+
+namespace bnr {
+namespace {
+
+constexpr int kRowsPerWg = 16;
+constexpr int kPass = 4096;                 // activations per LDS pass
+constexpr int kGroups = kPass / 16;         // 16-activation groups per pass
+constexpr int kPieces = kPass / 64;         // 16-byte weight pieces per row and pass
+constexpr int kPiecesPerLane = kPieces / 16;
+
+// Decode table for v_perm_b32: byte c of kCodeValue is the int8 value of
+// code c (+1, 0, -1, 0).
+constexpr unsigned kCodeValue = 0x00FF0001u;
+
+// One packed dword w = weights 16g .. 16g+15 (weight 16g + 4k + p at bits
+// 8k + 2p).  (w >> 2p) & 0x03030303 puts the codes of weights 4k + p,
+// k = 0..3, in its four bytes; v_perm maps each code to its value.  act.{x,y,z,w}
+// hold the activations of the same positions for p = 0, 1, 2, 3.
+__device__ __forceinline__ int dot16(unsigned w, uint4 act, int acc) {
+  const unsigned m = 0x03030303u;
+  acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(0u, kCodeValue, w & m), (int)act.x, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(0u, kCodeValue, (w >> 2) & m), (int)act.y, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(0u, kCodeValue, (w >> 4) & m), (int)act.z, acc, false);
+  acc = __builtin_amdgcn_sdot4((int)__builtin_amdgcn_perm(0u, kCodeValue, (w >> 6) & m), (int)act.w, acc, false);
+  return acc;
+}
+
+// 16 activations x0..x3 (dword t = activations 4t .. 4t+3) -> the four
+// dwords dot16 expects: dword p = activations p, 4+p, 8+p, 12+p (a 4x4 byte
+// transpose).
+__device__ __forceinline__ uint4 transpose_bytes(uint4 x) {
+  const unsigned t0 = __builtin_amdgcn_perm(x.y, x.x, 0x05010400u);  // x0b0 x1b0 x0b1 x1b1
+  const unsigned t1 = __builtin_amdgcn_perm(x.y, x.x, 0x07030602u);  // x0b2 x1b2 x0b3 x1b3
+  const unsigned t2 = __builtin_amdgcn_perm(x.w, x.z, 0x05010400u);  // x2b0 x3b0 x2b1 x3b1
+  const unsigned t3 = __builtin_amdgcn_perm(x.w, x.z, 0x07030602u);  // x2b2 x3b2 x2b3 x3b3
+  return make_uint4(__builtin_amdgcn_perm(t2, t0, 0x05040100u), __builtin_amdgcn_perm(t2, t0, 0x07060302u),
+                    __builtin_amdgcn_perm(t3, t1, 0x05040100u), __builtin_amdgcn_perm(t3, t1, 0x07060302u));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// Sum over the 16 lanes of a DPP row.
+__device__ __forceinline__ int row_sum16_i(int v) {
+  v += dpp_i<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_i<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_i<0x141>(v);  // row_half_mirror
+  v += dpp_i<0x140>(v);  // row_mirror
+  return v;
+}
+
+// Bytes [off, off+16) of p, the ones at or past `limit` read as zero.
+__device__ __forceinline__ uint4 load16_bounded(const uint8_t *p, long long off, long long limit) {
+  unsigned d[4] = {0u, 0u, 0u, 0u};
+  for (int b = 0; b < 16; ++b)
+    if (off + b < limit) d[b >> 2] |= (unsigned)p[off + b] << (8 * (b & 3));
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// VEC: rows start 16-byte aligned with a whole number of 16-byte pieces
+// (ceil(K/4) % 16 == 0) and the activations are 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void ternary_gemv_kernel(TernaryGemvArgs a) {
+  // Activations of the pass, transposed: group g (activations 16g..16g+15)
+  // at s_act[(g % 4) * kPieces + g / 4], so that the 16 lanes of a row read
+  // consecutive 16-byte slots.
+  __shared__ uint4 s_act[kGroups];
+  const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15;
+  const int row = blockIdx.x * kRowsPerWg + slot;
+  const long long prow = (long long)min(row, a.out_features - 1) * a.packed_cols;
+  const uint8_t *w = a.weight;
+  int acc = 0;
+  for (int k0 = 0; k0 < a.in_features; k0 += kPass) {
+    const int kn = min(kPass, a.in_features - k0);   // activations of this pass
+    const long long b0 = prow + k0 / 4;              // first packed byte of the pass
+    const int nb = (kn + 3) / 4;                     // packed bytes of the pass
+    uint4 wv[kPiecesPerLane];
+#pragma unroll
+    for (int i = 0; i < kPiecesPerLane; ++i) {
+      const int c = j + 16 * i;
+      if (VEC) {
+        wv[i] = 16 * c < nb ? *reinterpret_cast<const uint4 *>(w + b0 + 16 * c) : make_uint4(0, 0, 0, 0);
+      } else {
+        wv[i] = 16 * c < nb ? load16_bounded(w, b0 + 16 * c, b0 + nb) : make_uint4(0, 0, 0, 0);
+      }
+    }
+    __syncthreads();  // the previous pass has finished reading s_act
+    for (int g = tid; g < kGroups; g += 256) {
+      const int a0 = 16 * g;
+      uint4 x;
+      if (VEC && a0 + 16 <= kn) {
+        x = *reinterpret_cast<const uint4 *>(a.act + k0 + a0);
+      } else {
+        x = load16_bounded(reinterpret_cast<const uint8_t *>(a.act), (long long)k0 + a0,
+                           (long long)k0 + kn);
+      }
+      s_act[(g & 3) * kPieces + (g >> 2)] = transpose_bytes(x);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPiecesPerLane; ++i) {
+      const int c = j + 16 * i;
+      if (16 * c < nb) {
+        acc = dot16(wv[i].x, s_act[c], acc);
+        acc = dot16(wv[i].y, s_act[kPieces + c], acc);
+        acc = dot16(wv[i].z, s_act[2 * kPieces + c], acc);
+        acc = dot16(wv[i].w, s_act[3 * kPieces + c], acc);
+      }
+    }
+  }
+  acc = row_sum16_i(acc);
+  if (j == 0 && row < a.out_features) a.out[row] = (float)acc * a.scale;
+}
+
+}  // namespace
+
+hipError_t launch_ternary_gemv(const TernaryGemvArgs &a, bool vec, hipStream_t s) {
+  if (a.out_features <= 0) return hipSuccess;
+  const dim3 grid((a.out_features + kRowsPerWg - 1) / kRowsPerWg);
+  if (vec)
+    ternary_gemv_kernel<true><<<grid, dim3(256), 0, s>>>(a);
+  else
+    ternary_gemv_kernel<false><<<grid, dim3(256), 0, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace bnr

@@ -102,4 +102,17 @@ PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift);
 hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s);
 bool prefill_supported(int group);
 
+// W2A8 ternary GEMV: out[i] = (float)dot(W[i], act) * scale, W packed 2 bits
+// per weight, ceil(in_features/4) bytes per row.
+struct TernaryGemvArgs {
+  const uint8_t *weight;
+  const int8_t *act;
+  float *out;
+  long long packed_cols;
+  int out_features, in_features;
+  float scale;  // weight_scale * act_absmax / 127, rounded as the reference does
+};
+// vec: 16-byte aligned rows and activations, ceil(in_features/4) % 16 == 0.
+hipError_t launch_ternary_gemv(const TernaryGemvArgs &a, bool vec, hipStream_t s);
+
 }  // namespace bnr

@@ -2,14 +2,15 @@
  * bitnet_hip.h -- C ABI of the MI355X (gfx950) GQA attention hot path of
  * bitnetrs: RoPE (half-split, any theta) on Q/K, KV-cache append into an
  * HBM-resident head-major cache, split-K decode attention and causal
- * flash prefill.
+ * flash prefill; and the W2A8 ternary GEMV of the layer projections.
  *
  * Conventions
  *  - Every entry point returns an int status (BNR_OK == 0) and never aborts.
  *    On failure, bnr_last_error() returns the calling thread's message; its
  *    text follows BitNetError's Display strings
  *    (bitnet-core/src/error.rs:12-55).
- *  - "Host" entry points (bnr_rope_embed, bnr_masked_attention) take host
+ *  - "Host" entry points (bnr_rope_embed, bnr_masked_attention,
+ *    bnr_ternary_gemv_preq) take host
  *    slices exactly as the reference's Backend trait methods do and are
  *    synchronous: outputs are written when they return.
  *  - "Device" entry points (bnr_dev_*) take device pointers (HBM), are
@@ -39,6 +40,7 @@ extern "C" {
 #define BNR_INVALID_CONFIG 2     /* BitNetError::InvalidConfig           */
 #define BNR_BACKEND_ERROR 3      /* BitNetError::BackendError{"HIP",..}  */
 #define BNR_UNSUPPORTED_DEVICE 4 /* BitNetError::UnsupportedDevice       */
+#define BNR_QUANTIZATION_ERROR 5 /* BitNetError::QuantizationError       */
 
 typedef struct bnr_ctx bnr_ctx;
 
@@ -95,6 +97,24 @@ int bnr_masked_attention(bnr_ctx *ctx, const float *q, size_t q_len, const float
 int bnr_set_mirror_mode(bnr_ctx *ctx, int mode);
 /* Forget every mirror (call after rewriting rows other than the newest). */
 int bnr_mirror_invalidate(bnr_ctx *ctx);
+
+/* Backend::ternary_gemv_preq (bitnet-core/src/backend/mod.rs:445-468), as
+ * CpuBackend implements it (bitnet-cpu/src/lib.rs:519-538 ->
+ * gemv::ternary_gemv_quantised, bitnet-cpu/src/gemv.rs:368-430):
+ *   output[i] = (float)(sum_j W[i][j] * activation_q[j])
+ *               * (weight_scale * act_absmax / 127)
+ * with W packed 2 bits per weight, row-aligned (ceil(in_features/4) bytes
+ * per row; 0b00 -> +1, 0b01 -> 0, 0b10 -> -1, 0b11 -> 0).  The integer sum
+ * is exact, so outputs are bit-identical to the reference's.  Validation
+ * order and messages follow gemv.rs:384-420 (InvalidShape for lengths,
+ * QuantizationError for scales).  The weight matrix is mirrored in HBM on
+ * first use, keyed by (weight_packed, weight_len) and a 64-byte sample of
+ * its contents: model weights are immutable once loaded.  After rewriting a
+ * matrix in place, call bnr_mirror_invalidate (which drops these mirrors). */
+int bnr_ternary_gemv_preq(bnr_ctx *ctx, const uint8_t *weight_packed, size_t weight_len,
+                          float weight_scale, const int8_t *activation_q, size_t act_len,
+                          float act_absmax, float *output, size_t out_len,
+                          size_t out_features, size_t in_features);
 
 /* ----------------------------------------------------------------------- */
 /* Device entry points (HBM-resident cache, stream-ordered)                */
@@ -163,6 +183,14 @@ int bnr_dev_prefill(bnr_ctx *ctx, float *q, float *k, const float *v, size_t n_t
                     size_t start_pos, size_t n_heads, size_t n_kv_heads, size_t head_dim,
                     float theta, float *k_cache, float *v_cache, size_t cap, float *out,
                     void *stream);
+
+/* ternary_gemv_preq on device pointers: weight_packed
+ * [out_features x ceil(in_features/4)] bytes, activation_q [in_features],
+ * output [out_features].  Same arithmetic and scale checks as
+ * bnr_ternary_gemv_preq. */
+int bnr_dev_ternary_gemv_preq(bnr_ctx *ctx, const uint8_t *weight_packed, float weight_scale,
+                              const int8_t *activation_q, float act_absmax, float *output,
+                              size_t out_features, size_t in_features, void *stream);
 
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);

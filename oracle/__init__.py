@@ -19,7 +19,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libbnr_oracle.so")
 
-OK, INVALID_SHAPE, INVALID_CONFIG, BACKEND_ERROR = 0, 1, 2, 3
+OK, INVALID_SHAPE, INVALID_CONFIG, BACKEND_ERROR, QUANTIZATION_ERROR = 0, 1, 2, 3, 5
 
 
 class OracleError(Exception):
@@ -40,7 +40,12 @@ class BackendError(OracleError):
     kind = BACKEND_ERROR
 
 
-_ERR = {INVALID_SHAPE: InvalidShape, INVALID_CONFIG: InvalidConfig, BACKEND_ERROR: BackendError}
+class QuantizationError(OracleError):
+    kind = QUANTIZATION_ERROR
+
+
+_ERR = {INVALID_SHAPE: InvalidShape, INVALID_CONFIG: InvalidConfig, BACKEND_ERROR: BackendError,
+        QUANTIZATION_ERROR: QuantizationError}
 
 
 def build() -> str:
@@ -102,6 +107,12 @@ def _declare(L: ctypes.CDLL) -> None:
                                     _sz, _sz, _sz, ctypes.c_float, _f]
     L.bnro_set_threads.argtypes = [ctypes.c_int]
     L.bnro_get_threads.restype = ctypes.c_int
+    _u8 = ctypes.c_void_p
+    L.bnro_pack_ternary.argtypes = [_u8, _sz, _u8]
+    L.bnro_dot_packed_ternary_i8.argtypes = [_u8, _u8, _sz]
+    L.bnro_dot_packed_ternary_i8.restype = ctypes.c_int32
+    L.bnro_ternary_gemv_preq.argtypes = [_u8, _sz, ctypes.c_float, _u8, _sz, ctypes.c_float, _f,
+                                         _sz, _sz, _sz]
 
 
 def _check(status: int) -> None:
@@ -277,3 +288,44 @@ def layer_tokens(backend: CpuBackend, cache: KVCache, layer, q_raw, k_raw, v_raw
                                    _ptr(v_raw), n, start_pos, n_heads, n_kv_heads, head_dim,
                                    theta, _ptr(out)))
     return out
+
+
+# ----------------------------------------------------------------------------
+# W2A8 ternary GEMV
+# ----------------------------------------------------------------------------
+
+def _bytes_ptr(a: np.ndarray, dtype) -> ctypes.c_void_p:
+    if a.dtype != dtype or not a.flags.c_contiguous:
+        raise TypeError(f"oracle arrays must be C-contiguous {np.dtype(dtype).name}")
+    return ctypes.c_void_p(a.ctypes.data if a.size else 0)
+
+
+def pack_ternary(w: np.ndarray) -> np.ndarray:
+    """pack_ternary (bitnet-core/src/quant/ternary.rs:266-286) of one row."""
+    w = np.ascontiguousarray(w, np.int8)
+    out = np.zeros((w.size + 3) // 4, np.uint8)
+    _check(lib().bnro_pack_ternary(_bytes_ptr(w, np.int8), w.size, _bytes_ptr(out, np.uint8)))
+    return out
+
+
+def pack_rows(w: np.ndarray) -> np.ndarray:
+    """Row-aligned packing of a [rows, cols] ternary matrix (each row padded
+    to ceil(cols/4) bytes), as the model's weight loader stores it."""
+    return np.stack([pack_ternary(r) for r in np.asarray(w, np.int8)]) if len(w) else \
+        np.zeros((0, (np.asarray(w).shape[1] + 3) // 4), np.uint8)
+
+
+def dot_packed_ternary_i8(packed: np.ndarray, act: np.ndarray, n: int) -> int:
+    return int(lib().bnro_dot_packed_ternary_i8(_bytes_ptr(packed, np.uint8),
+                                                _bytes_ptr(act, np.int8), n))
+
+
+def ternary_gemv_preq(weight_packed, weight_scale, activation_q, act_absmax, output,
+                      out_features, in_features) -> None:
+    """CpuBackend::ternary_gemv_preq (bitnet-cpu/src/lib.rs:519-538 ->
+    gemv::ternary_gemv_quantised, gemv.rs:368-430)."""
+    w = np.ascontiguousarray(weight_packed, np.uint8).reshape(-1)
+    a = np.ascontiguousarray(activation_q, np.int8).reshape(-1)
+    _check(lib().bnro_ternary_gemv_preq(_bytes_ptr(w, np.uint8), w.size, weight_scale,
+                                        _bytes_ptr(a, np.int8), a.size, act_absmax,
+                                        _ptr(output), output.size, out_features, in_features))

@@ -49,6 +49,52 @@ static int ok(void) {
   return BNRO_OK;
 }
 
+static int fail_quant(const char *msg) {
+  snprintf(g_err, sizeof g_err, "quantization error: %s", msg);
+  return BNRO_QUANTIZATION_ERROR;
+}
+
+/* Rust's Display of an f32: the shortest decimal that reads back to the same
+ * value, written positionally ("0.5", "-3", "0.0000001", "NaN", "inf"). */
+static void rust_f32(char *buf, size_t cap, float x) {
+  if (isnan(x)) { snprintf(buf, cap, "NaN"); return; }
+  if (isinf(x)) { snprintf(buf, cap, x < 0 ? "-inf" : "inf"); return; }
+  if (x == 0.0f) { snprintf(buf, cap, signbit(x) ? "-0" : "0"); return; }
+  char e[64];
+  int p = 1;
+  for (; p <= 9; ++p) {
+    snprintf(e, sizeof e, "%.*e", p - 1, (double)x);
+    if ((float)strtod(e, NULL) == x) break;
+  }
+  /* e = [-]d[.ddd]e[+-]XX */
+  char digits[16];
+  int nd = 0, neg = e[0] == '-';
+  const char *q = e + neg;
+  for (; *q && *q != 'e'; ++q)
+    if (*q != '.') digits[nd++] = *q;
+  const int ex = atoi(q + 1);
+  while (nd > 1 && digits[nd - 1] == '0') --nd;
+  char out[128];
+  int o = 0;
+  if (neg) out[o++] = '-';
+  if (ex >= nd - 1) {
+    for (int i = 0; i < nd; ++i) out[o++] = digits[i];
+    for (int i = 0; i < ex - (nd - 1); ++i) out[o++] = '0';
+  } else if (ex >= 0) {
+    for (int i = 0; i < nd; ++i) {
+      out[o++] = digits[i];
+      if (i == ex) out[o++] = '.';
+    }
+  } else {
+    out[o++] = '0';
+    out[o++] = '.';
+    for (int i = 0; i < -ex - 1; ++i) out[o++] = '0';
+    for (int i = 0; i < nd; ++i) out[o++] = digits[i];
+  }
+  out[o] = 0;
+  snprintf(buf, cap, "%s", out);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Seeded generator                                                          */
 /* ------------------------------------------------------------------------ */
@@ -188,7 +234,7 @@ int bnro_rope_table(size_t max_seq, size_t head_dim, float theta, float *cos_out
   if (head_dim == 0 || head_dim % 2 != 0)
     return fail_config("head_dim must be even and > 0, got %zu", head_dim);
   if (!(theta > 0.0f) || !isfinite(theta))
-    return fail_config("theta must be finite and > 0, got %g", (double)theta);
+    { char tf[64]; rust_f32(tf, sizeof tf, theta); return fail_config("theta must be finite and > 0, got %s", tf); }
   size_t half = head_dim / 2;
   for (size_t pos = 0; pos < max_seq; pos++)
     for (size_t i = 0; i < half; i++)
@@ -234,7 +280,7 @@ int bnro_apply_rope(float *q, size_t q_len, float *k, size_t k_len, size_t posit
     return fail_shape("head_dim must be even and > 0", g);
   }
   if (!(theta > 0.0f) || !isfinite(theta))
-    return fail_config("theta must be finite and > 0, got %g", (double)theta);
+    { char tf[64]; rust_f32(tf, sizeof tf, theta); return fail_config("theta must be finite and > 0, got %s", tf); }
   int st = check_qk_len(q_len, k_len, n_heads, n_kv_heads, head_dim);
   if (st) return st;
   size_t half = head_dim / 2;
@@ -551,6 +597,119 @@ int bnro_layer_tokens(bnro_backend *b, bnro_kv_cache *c, size_t layer, float *q_
     st = bnro_masked_attention(q, qd, c->k[layer], backing, c->v[layer], backing,
                                out + i * qd, qd, n_heads, n_kv_heads, head_dim, pos);
     if (st) return st;
+  }
+  return ok();
+}
+
+/* ------------------------------------------------------------------------ */
+/* W2A8 ternary GEMV                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* ternary.rs:266-286 */
+int bnro_pack_ternary(const int8_t *w, size_t n, uint8_t *out) {
+  const size_t nb = (n + 3) / 4;
+  memset(out, 0, nb);
+  for (size_t i = 0; i < n; ++i) {
+    unsigned code;
+    switch (w[i]) {
+      case 1: code = 0; break;
+      case 0: code = 1; break;
+      case -1: code = 2; break;
+      default:
+        return fail_config("ternary value out of range");
+    }
+    out[i / 4] |= (uint8_t)(code << (2 * (i % 4)));
+  }
+  return ok();
+}
+
+/* DECODE_LUT (simd.rs:390-404): code -> value, 0b11 decodes to 0. */
+static const int8_t kTernaryCode[4] = {1, 0, -1, 0};
+
+static void unpack_packed_to_i8(const uint8_t *packed, int8_t *out, size_t n) {
+  for (size_t i = 0; i < n; ++i) out[i] = kTernaryCode[(packed[i / 4] >> (2 * (i % 4))) & 3];
+}
+
+/* dot_ternary_i8_avx2 (simd.rs:118-171): sign-extend to i16, vpsignw,
+ * vpmaddwd against ones, i32 lanes, then the scalar tail.  Exact integer
+ * arithmetic, so the lane order does not change the result. */
+static int32_t dot_ternary_i8_avx2(const int8_t *w, const int8_t *a, size_t len) {
+  const size_t chunks = len / 16;
+  const __m256i ones = _mm256_set1_epi16(1);
+  __m256i acc = _mm256_setzero_si256();
+  for (size_t i = 0; i < chunks; ++i) {
+    const __m256i w16 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i *)(w + 16 * i)));
+    const __m256i a16 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i *)(a + 16 * i)));
+    acc = _mm256_add_epi32(acc, _mm256_madd_epi16(_mm256_sign_epi16(a16, w16), ones));
+  }
+  int32_t lanes[8];
+  _mm256_storeu_si256((__m256i *)lanes, acc);
+  int32_t r = 0;
+  for (int i = 0; i < 8; ++i) r += lanes[i];
+  for (size_t i = chunks * 16; i < len; ++i) r += (int32_t)w[i] * (int32_t)a[i];
+  return r;
+}
+
+/* simd.rs:461-500: 64-element chunks decoded into a stack buffer. */
+int32_t bnro_dot_packed_ternary_i8(const uint8_t *packed, const int8_t *act, size_t n) {
+  int8_t buf[64];
+  int32_t total = 0;
+  const size_t full = n / 64, rem = n % 64;
+  for (size_t c = 0; c < full; ++c) {
+    unpack_packed_to_i8(packed + 16 * c, buf, 64);
+    total += dot_ternary_i8_avx2(buf, act + 64 * c, 64);
+  }
+  if (rem) {
+    unpack_packed_to_i8(packed + 16 * full, buf, rem);
+    for (size_t i = 0; i < rem; ++i) total += (int32_t)buf[i] * (int32_t)act[64 * full + i];
+  }
+  return total;
+}
+
+/* gemv.rs:368-430 (validation order and messages as there). */
+int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, float weight_scale,
+                           const int8_t *activation_q, size_t act_len, float act_absmax,
+                           float *output, size_t out_len, size_t out_features,
+                           size_t in_features) {
+  char e[160], g[96], f[64];
+  const size_t packed_cols = (in_features + 3) / 4;
+  if (packed_cols != 0 && out_features > SIZE_MAX / packed_cols)
+    return fail_shape("weight size fits usize", "overflow");
+  const size_t expected = out_features * packed_cols;
+  if (weight_len != expected) {
+    snprintf(e, sizeof e, "weight_packed.len() == %zu * ceil(%zu/4) = %zu", out_features,
+             in_features, expected);
+    snprintf(g, sizeof g, "weight_packed.len() == %zu", weight_len);
+    return fail_shape(e, g);
+  }
+  if (act_len != in_features) {
+    snprintf(e, sizeof e, "activation.len() == %zu", in_features);
+    snprintf(g, sizeof g, "activation.len() == %zu", act_len);
+    return fail_shape(e, g);
+  }
+  if (out_len != out_features) {
+    snprintf(e, sizeof e, "output.len() == %zu", out_features);
+    snprintf(g, sizeof g, "output.len() == %zu", out_len);
+    return fail_shape(e, g);
+  }
+  if (weight_scale <= 0.0f || !isfinite(weight_scale)) {
+    rust_f32(f, sizeof f, weight_scale);
+    snprintf(e, sizeof e, "weight_scale must be finite > 0, got %s", f);
+    return fail_quant(e);
+  }
+  if (act_absmax <= 0.0f || !isfinite(act_absmax)) {
+    rust_f32(f, sizeof f, act_absmax);
+    snprintf(e, sizeof e, "act_scale must be finite > 0, got %s", f);
+    return fail_quant(e);
+  }
+  /* combined_scale = weight_scale * act_scale / 127.0 (left to right, f32) */
+  const float combined = weight_scale * act_absmax / 127.0f;
+  const int nthr = bnro_get_threads();
+#pragma omp parallel for num_threads(nthr) schedule(static)
+  for (size_t i = 0; i < out_features; ++i) {
+    const int32_t acc =
+        bnro_dot_packed_ternary_i8(weight_packed + i * packed_cols, activation_q, in_features);
+    output[i] = (float)acc * combined;
   }
   return ok();
 }

@@ -27,6 +27,7 @@ extern "C" {
 #define BNRO_INVALID_SHAPE 1
 #define BNRO_INVALID_CONFIG 2
 #define BNRO_BACKEND_ERROR 3
+#define BNRO_QUANTIZATION_ERROR 5
 
 /* Last error message of the calling thread ("" after success). */
 const char *bnro_last_error(void);
@@ -104,6 +105,25 @@ int bnro_layer_tokens(bnro_backend *b, bnro_kv_cache *c, size_t layer, float *q_
                       float *k_raw, const float *v_raw, size_t n_tokens,
                       size_t start_pos, size_t n_heads, size_t n_kv_heads,
                       size_t head_dim, float theta, float *out);
+
+/* ---- W2A8 ternary GEMV (the next component after attention) ---- */
+
+/* pack_ternary  bitnet-core/src/quant/ternary.rs:266-286: n values in
+ * {-1,0,+1} -> ceil(n/4) bytes, value i at bits 2(i%4) of byte i/4,
+ * +1 -> 0b00, 0 -> 0b01, -1 -> 0b10, unused positions 0b00. */
+int bnro_pack_ternary(const int8_t *w, size_t n, uint8_t *out);
+/* simd::dot_packed_ternary_i8_fast  bitnet-cpu/src/simd.rs:511-531
+ * (AVX2 body dot_packed_ternary_i8_avx2_chunked 461-500, LUT decode
+ * DECODE_LUT 390-404 with code 0b11 -> 0, dot_ternary_i8_avx2 118-171):
+ * exact i32 sum of decoded weight x activation over n elements. */
+int32_t bnro_dot_packed_ternary_i8(const uint8_t *packed, const int8_t *act, size_t n);
+/* gemv::ternary_gemv_quantised  bitnet-cpu/src/gemv.rs:368-430, which is
+ * CpuBackend::ternary_gemv_preq (bitnet-cpu/src/lib.rs:519-538):
+ * out[i] = (float)dot(W[i], act) * (weight_scale * act_absmax / 127). */
+int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, float weight_scale,
+                           const int8_t *activation_q, size_t act_len, float act_absmax,
+                           float *output, size_t out_len, size_t out_features,
+                           size_t in_features);
 
 /* Number of OpenMP threads the attention head loop uses (Rayon sizes its
  * pool to all logical cores, lib.rs:99-133). 0 = all cores. */
