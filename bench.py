@@ -269,6 +269,107 @@ def bench_batched(torch, be, steps: int = 50, n_seq: int = 32, cap: int = 4096):
             "lengths_min_max_mean": [int(lens.min()), int(lens.max()), float(lens.mean())]}
 
 
+# The seven ternary projections of one BitNet b1.58 2B layer for one token:
+# (out_features, in_features) of q, k, v, o, gate, up, down.
+GEMV_SHAPES = [(2560, 2560), (640, 2560), (640, 2560), (2560, 2560), (6912, 2560),
+               (6912, 2560), (2560, 6912)]
+
+
+def gemv_bytes(m: int, k: int) -> int:
+    """Packed weights (ceil(k/4) bytes per row) + int8 activations + f32 outputs."""
+    return m * ((k + 3) // 4) + k + 4 * m
+
+
+def bench_gemv(torch, be, steps: int = 20, n_layers: int = 30):
+    """W2A8 ternary GEMV: the 7 projections of every layer for one decode
+    token (30 layers x 17.4 MB of packed weights = 522 MB, more than the
+    256 MB MALL), one HIP graph of 210 launches per token.  Weights are
+    random bytes (every 2-bit code, 0b11 included), activations random int8."""
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7060)
+    ws = [[torch.randint(0, 256, (m * ((k + 3) // 4),), dtype=torch.uint8, device="cuda",
+                         generator=g) for (m, k) in GEMV_SHAPES] for _ in range(n_layers)]
+    acts = [torch.randint(-128, 128, (k,), dtype=torch.int8, device="cuda", generator=g)
+            for (_, k) in GEMV_SHAPES]
+    outs = [torch.zeros(m, device="cuda") for (m, _) in GEMV_SHAPES]
+
+    def token():  # q/k/v and gate/up share their activation: one grouped launch each
+        for layer in range(n_layers):
+            w = ws[layer]
+            be.dev_ternary_gemv_preq_group(w[0:3], [0.75] * 3, acts[0], 11.0, outs[0:3],
+                                           [2560, 640, 640], 2560)
+            be.dev_ternary_gemv_preq(w[3], 0.75, acts[3], 11.0, outs[3], 2560, 2560)
+            be.dev_ternary_gemv_preq_group(w[4:6], [0.75] * 2, acts[4], 11.0, outs[4:6],
+                                           [6912, 6912], 2560)
+            be.dev_ternary_gemv_preq(w[6], 0.75, acts[6], 11.0, outs[6], 2560, 6912)
+
+    def token_separate():  # one launch per projection, as the trait calls them
+        for layer in range(n_layers):
+            for i, (m, k) in enumerate(GEMV_SHAPES):
+                be.dev_ternary_gemv_preq(ws[layer][i], 0.75, acts[i], 11.0, outs[i], m, k)
+
+    def gate_only():  # the dominant launch (6912 x 2560), over the 30 layers' gate weights
+        for layer in range(n_layers):
+            be.dev_ternary_gemv_preq(ws[layer][4], 0.75, acts[4], 11.0, outs[4], 6912, 2560)
+
+    res = {}
+    for name, fn, launches in (("token", token, n_layers * 4),
+                               ("separate", token_separate, n_layers * len(GEMV_SHAPES)),
+                               ("gate", gate_only, n_layers)):
+        fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        res[name] = t0.elapsed_time(t1) / steps
+        res[name + "_launches"] = launches
+    tok_bytes = n_layers * sum(gemv_bytes(m, k) for (m, k) in GEMV_SHAPES)
+    gate_bytes = gemv_bytes(6912, 2560)
+    gate_us = res["gate"] * 1e3 / n_layers
+    del ws
+    torch.cuda.empty_cache()
+    return {"token_ms": res["token"], "token_bytes": tok_bytes,
+            "gbs": tok_bytes / (res["token"] * 1e-3) / 1e9,
+            "launch_us": res["token"] * 1e3 / res["token_launches"],
+            "separate_ms": res["separate"],
+            "gate_us": gate_us, "gate_bytes": gate_bytes,
+            "gate_gbs": gate_bytes / (gate_us * 1e-6) / 1e9}
+
+
+def cpu_baseline_gemv(budget_s: float):
+    """The oracle's ternary_gemv_preq (AVX2 integer dot, rows over all host
+    cores) on the 7 projections of one layer for one token, repeated."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0xB17E7061)
+    mats = [(rng.integers(0, 256, size=m * ((k + 3) // 4)).astype(np.uint8),
+             rng.integers(-128, 128, size=k).astype(np.int8), np.zeros(m, np.float32), m, k)
+            for (m, k) in GEMV_SHAPES]
+    n, t_start = 0, time.perf_counter()
+    while True:
+        for w, a, o, m, k in mats:
+            oracle.ternary_gemv_preq(w, 0.75, a, 11.0, o, m, k)
+        n += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    dt = (time.perf_counter() - t_start) / n
+    layer_bytes = sum(gemv_bytes(m, k) for (m, k) in GEMV_SHAPES)
+    return {"value": layer_bytes / dt / 1e9, "unit": "GB/s", "cores": oracle.get_threads(),
+            "kind": "port",
+            "sample": f"{n} x the 7 ternary projections of one 2B layer for one token "
+                      f"({layer_bytes} B), {dt * 1e3:.3f} ms each"}
+
+
 def copy_calibration(torch, nbytes: int = 256 << 20, reps: int = 5) -> None:
     """Plain device-to-device copies of a known size: the reference for
     scaling FETCH_SIZE / WRITE_SIZE counters in a --pmc run of this script."""
@@ -354,6 +455,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack workload")
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the ternary GEMV workload")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -441,11 +543,30 @@ def main() -> int:
             "prefill_flops": stk["prefill_flops"],
             "note": "decode timed as one HIP graph of 7680 fused decode launches; caches total "
                     "197 MB, which fits the 256 MB MALL"}
+    if not args.no_gemv:
+        gm = bench_gemv(torch, be)
+        log(f"ternary gemv: token (30 layers x 7 projections, 4 launches per layer) "
+            f"{gm['token_ms']:.3f} ms, {gm['gbs']:.0f} GB/s; 7 launches per layer "
+            f"{gm['separate_ms']:.3f} ms; gate 6912x2560 {gm['gate_us']:.2f} us, "
+            f"{gm['gate_gbs']:.0f} GB/s")
+        line["gemv"] = {
+            "workload": "bitnet_2b_ternary_gemv_token_30L_x7proj_w2a8",
+            "value": round(gm["gbs"], 2), "unit": "GB/s", "ms_per_token": round(gm["token_ms"], 4),
+            "bytes_per_token": gm["token_bytes"], "launch_us": round(gm["launch_us"], 3),
+            "launches_per_layer": 4, "ms_per_token_7_launches": round(gm["separate_ms"], 4),
+            "roofline": {"bound": "hbm", "achieved": round(gm["gate_gbs"], 2),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gm["gate_gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("ternary_gemv_kernel", {}).get("bytes_per_launch"),
+                         "kernel": "ternary_gemv_kernel (6912 x 2560)",
+                         "kernel_us": round(gm["gate_us"], 3), "bytes_per_launch": gm["gate_bytes"]}}
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)
         if not args.no_prefill:
             line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(args.cpu_budget)
+        if not args.no_gemv:
+            line["gemv"]["cpu_baseline"] = cpu_baseline_gemv(min(args.cpu_budget, 5.0))
     be.close()
     print(json.dumps(line), flush=True)
     return 0

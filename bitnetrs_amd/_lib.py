@@ -102,6 +102,9 @@ SIGNATURES = {
                                          _sz, _sz, _sz]),
     "bnr_dev_ternary_gemv_preq": (_c.c_int, [_vp, _vp, _c.c_float, _vp, _c.c_float, _vp, _sz,
                                              _sz, _vp]),
+    "bnr_dev_ternary_gemv_preq_group": (_c.c_int, [_vp, _sz, _c.POINTER(_vp), _f, _vp,
+                                                   _c.c_float, _c.POINTER(_vp),
+                                                   _c.POINTER(_sz), _sz, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
 }
 

@@ -183,6 +183,20 @@ class HipBackend:
             _dev(activation_q, "activation_q", dtype=torch.int8), act_absmax,
             _dev(output, "output"), out_features, in_features, _stream(stream)))
 
+    def dev_ternary_gemv_preq_group(self, weights, weight_scales, activation_q, act_absmax,
+                                    outputs, out_features, in_features, stream=None) -> None:
+        """Several ternary GEMVs sharing one activation vector, one launch."""
+        import torch
+
+        n = len(weights)
+        wp = (ctypes.c_void_p * n)(*[_dev(w, "weight", dtype=torch.uint8).value for w in weights])
+        op = (ctypes.c_void_p * n)(*[_dev(o, "output").value for o in outputs])
+        sc = (ctypes.c_float * n)(*[float(x) for x in weight_scales])
+        mf = (ctypes.c_size_t * n)(*[int(x) for x in out_features])
+        _lib.check(self._L.bnr_dev_ternary_gemv_preq_group(
+            self._h, n, wp, sc, _dev(activation_q, "activation_q", dtype=torch.int8), act_absmax,
+            op, mf, in_features, _stream(stream)))
+
     def dev_synchronize(self, stream=None) -> None:
         _lib.check(self._L.bnr_dev_synchronize(self._h, _stream(stream)))
 

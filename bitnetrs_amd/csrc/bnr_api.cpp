@@ -1259,6 +1259,46 @@ extern "C" int bnr_dev_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packe
   return set_ok();
 }
 
+extern "C" int bnr_dev_ternary_gemv_preq_group(bnr_ctx *c, size_t n,
+                                               const uint8_t *const *weight_packed,
+                                               const float *weight_scales,
+                                               const int8_t *activation_q, float act_absmax,
+                                               float *const *outputs, const size_t *out_features,
+                                               size_t in_features, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (n == 0 || n > (size_t)kMaxGemvGroup)
+    return err_config(fmt("ternary GEMV group size must be 1..%d, got %zu", kMaxGemvGroup, n));
+  if (!weight_packed || !weight_scales || !outputs || !out_features)
+    return err_backend("ternary_gemv_preq_group: NULL array");
+  TernaryGemvGroupArgs g{};
+  g.n = (int)n;
+  g.act = activation_q;
+  g.in_features = (int)in_features;
+  g.packed_cols = (long long)((in_features + 3) / 4);
+  bool vec = g.packed_cols % 16 == 0 && ((uintptr_t)activation_q % 16) == 0;
+  int wgs = 0;
+  for (size_t i = 0; i < n; ++i) {
+    int st = check_gemv(SIZE_MAX, weight_scales[i], SIZE_MAX, act_absmax, SIZE_MAX,
+                        out_features[i], in_features);
+    if (st) return st;
+    if (out_features[i] && ((in_features && (!weight_packed[i] || !activation_q)) || !outputs[i]))
+      return err_backend("ternary_gemv_preq_group: NULL pointer");
+    g.weight[i] = weight_packed[i];
+    g.out[i] = outputs[i];
+    volatile float ws_as = weight_scales[i] * act_absmax;
+    g.scale[i] = ws_as / 127.0f;
+    g.out_features[i] = (int)out_features[i];
+    g.wg_off[i] = wgs;
+    wgs += (int)((out_features[i] + 15) / 16);
+    vec = vec && ((uintptr_t)weight_packed[i] % 16) == 0;
+  }
+  for (size_t i = n; i <= (size_t)kMaxGemvGroup; ++i) g.wg_off[i] = wgs;
+  if (wgs == 0) return set_ok();
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_ternary_gemv_group(g, vec, (hipStream_t)stream), "ternary_gemv group launch");
+  return set_ok();
+}
+
 extern "C" int bnr_dev_synchronize(bnr_ctx *c, void *stream) {
   if (!c) return err_backend("context is NULL");
   DeviceGuard dg(c->device);

@@ -76,21 +76,20 @@ __device__ __forceinline__ uint4 load16_bounded(const uint8_t *p, long long off,
   return make_uint4(d[0], d[1], d[2], d[3]);
 }
 
+// Rows [16*wg, 16*wg+16) of one matrix: out[row] = (float)dot * scale.
 // VEC: rows start 16-byte aligned with a whole number of 16-byte pieces
 // (ceil(K/4) % 16 == 0) and the activations are 16-byte aligned.
 template <bool VEC>
-__global__ __launch_bounds__(256) void ternary_gemv_kernel(TernaryGemvArgs a) {
-  // Activations of the pass, transposed: group g (activations 16g..16g+15)
-  // at s_act[(g % 4) * kPieces + g / 4], so that the 16 lanes of a row read
-  // consecutive 16-byte slots.
-  __shared__ uint4 s_act[kGroups];
+__device__ __forceinline__ void gemv_rows(const uint8_t *w, const int8_t *act, float *out,
+                                          int out_features, int in_features,
+                                          long long packed_cols, float scale, int wg,
+                                          uint4 *s_act) {
   const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15;
-  const int row = blockIdx.x * kRowsPerWg + slot;
-  const long long prow = (long long)min(row, a.out_features - 1) * a.packed_cols;
-  const uint8_t *w = a.weight;
+  const int row = wg * kRowsPerWg + slot;
+  const long long prow = (long long)min(row, out_features - 1) * packed_cols;
   int acc = 0;
-  for (int k0 = 0; k0 < a.in_features; k0 += kPass) {
-    const int kn = min(kPass, a.in_features - k0);   // activations of this pass
+  for (int k0 = 0; k0 < in_features; k0 += kPass) {
+    const int kn = min(kPass, in_features - k0);     // activations of this pass
     const long long b0 = prow + k0 / 4;              // first packed byte of the pass
     const int nb = (kn + 3) / 4;                     // packed bytes of the pass
     uint4 wv[kPiecesPerLane];
@@ -108,9 +107,9 @@ __global__ __launch_bounds__(256) void ternary_gemv_kernel(TernaryGemvArgs a) {
       const int a0 = 16 * g;
       uint4 x;
       if (VEC && a0 + 16 <= kn) {
-        x = *reinterpret_cast<const uint4 *>(a.act + k0 + a0);
+        x = *reinterpret_cast<const uint4 *>(act + k0 + a0);
       } else {
-        x = load16_bounded(reinterpret_cast<const uint8_t *>(a.act), (long long)k0 + a0,
+        x = load16_bounded(reinterpret_cast<const uint8_t *>(act), (long long)k0 + a0,
                            (long long)k0 + kn);
       }
       s_act[(g & 3) * kPieces + (g >> 2)] = transpose_bytes(x);
@@ -128,10 +127,53 @@ __global__ __launch_bounds__(256) void ternary_gemv_kernel(TernaryGemvArgs a) {
     }
   }
   acc = row_sum16_i(acc);
-  if (j == 0 && row < a.out_features) a.out[row] = (float)acc * a.scale;
+  if (j == 0 && row < out_features) out[row] = (float)acc * scale;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void ternary_gemv_kernel(TernaryGemvArgs a) {
+  // Activations of the pass, transposed: group g (activations 16g..16g+15)
+  // at s_act[(g % 4) * kPieces + g / 4], so that the 16 lanes of a row read
+  // consecutive 16-byte slots.
+  __shared__ uint4 s_act[kGroups];
+  gemv_rows<VEC>(a.weight, a.act, a.out, a.out_features, a.in_features, a.packed_cols, a.scale,
+                 blockIdx.x, s_act);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGroupArgs a) {
+  __shared__ uint4 s_act[kGroups];
+  const int b = blockIdx.x;
+  // Matrix of this workgroup, selected with constant indices so that the
+  // argument arrays stay in scalar registers.
+  const uint8_t *w = a.weight[0];
+  float *out = a.out[0];
+  float scale = a.scale[0];
+  int m = a.out_features[0], off = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGemvGroup; ++i) {
+    if (i < a.n && b >= a.wg_off[i]) {
+      w = a.weight[i];
+      out = a.out[i];
+      scale = a.scale[i];
+      m = a.out_features[i];
+      off = a.wg_off[i];
+    }
+  }
+  gemv_rows<VEC>(w, a.act, out, m, a.in_features, a.packed_cols, scale, b - off, s_act);
 }
 
 }  // namespace
+
+hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s) {
+  const int wgs = a.wg_off[a.n];
+  if (wgs <= 0) return hipSuccess;
+  if (vec)
+    ternary_gemv_group_kernel<true><<<dim3(wgs), dim3(256), 0, s>>>(a);
+  else
+    ternary_gemv_group_kernel<false><<<dim3(wgs), dim3(256), 0, s>>>(a);
+  return hipGetLastError();
+}
 
 hipError_t launch_ternary_gemv(const TernaryGemvArgs &a, bool vec, hipStream_t s) {
   if (a.out_features <= 0) return hipSuccess;

@@ -115,4 +115,19 @@ struct TernaryGemvArgs {
 // vec: 16-byte aligned rows and activations, ceil(in_features/4) % 16 == 0.
 hipError_t launch_ternary_gemv(const TernaryGemvArgs &a, bool vec, hipStream_t s);
 
+// Several ternary matrices that share one activation vector (q/k/v, or
+// gate/up) in one launch: matrix i owns workgroups wg_off[i] .. wg_off[i+1]-1.
+constexpr int kMaxGemvGroup = 8;
+struct TernaryGemvGroupArgs {
+  const uint8_t *weight[kMaxGemvGroup];
+  float *out[kMaxGemvGroup];
+  float scale[kMaxGemvGroup];
+  int out_features[kMaxGemvGroup];
+  int wg_off[kMaxGemvGroup + 1];
+  const int8_t *act;
+  long long packed_cols;
+  int in_features, n;
+};
+hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s);
+
 }  // namespace bnr

@@ -192,6 +192,19 @@ int bnr_dev_ternary_gemv_preq(bnr_ctx *ctx, const uint8_t *weight_packed, float 
                               const int8_t *activation_q, float act_absmax, float *output,
                               size_t out_features, size_t in_features, void *stream);
 
+/* Several ternary_gemv_preq calls that share one activation vector, in one
+ * launch: the q/k/v projections of BitNetModel::forward
+ * (bitnet-model/src/lib.rs:645-680) or gate/up (lib.rs:762-786).  Matrix i
+ * is weight_packed[i] [out_features[i] x ceil(in_features/4)] with scale
+ * weight_scales[i], written to outputs[i]; 1 <= n <= 8; the three arrays
+ * are host memory, the pointers in them device memory.  Results equal n
+ * separate bnr_dev_ternary_gemv_preq calls. */
+int bnr_dev_ternary_gemv_preq_group(bnr_ctx *ctx, size_t n, const uint8_t *const *weight_packed,
+                                    const float *weight_scales, const int8_t *activation_q,
+                                    float act_absmax, float *const *outputs,
+                                    const size_t *out_features, size_t in_features,
+                                    void *stream);
+
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
 

@@ -623,11 +623,24 @@ int bnro_pack_ternary(const int8_t *w, size_t n, uint8_t *out) {
   return ok();
 }
 
-/* DECODE_LUT (simd.rs:390-404): code -> value, 0b11 decodes to 0. */
+/* DECODE_LUT (simd.rs:390-404): byte -> its four values, code 0b11 -> 0. */
 static const int8_t kTernaryCode[4] = {1, 0, -1, 0};
+static int8_t g_decode_lut[256][4];
+static int g_decode_lut_ready;
 
+static void build_decode_lut(void) {
+  for (int b = 0; b < 256; ++b)
+    for (int p = 0; p < 4; ++p) g_decode_lut[b][p] = kTernaryCode[(b >> (2 * p)) & 3];
+  __atomic_store_n(&g_decode_lut_ready, 1, __ATOMIC_RELEASE);
+}
+
+/* unpack_packed_to_i8 (simd.rs:417-446): whole bytes through the LUT, then
+ * the remainder of the last byte. */
 static void unpack_packed_to_i8(const uint8_t *packed, int8_t *out, size_t n) {
-  for (size_t i = 0; i < n; ++i) out[i] = kTernaryCode[(packed[i / 4] >> (2 * (i % 4))) & 3];
+  if (!__atomic_load_n(&g_decode_lut_ready, __ATOMIC_ACQUIRE)) build_decode_lut();
+  const size_t full = n / 4, rem = n % 4;
+  for (size_t i = 0; i < full; ++i) memcpy(out + 4 * i, g_decode_lut[packed[i]], 4);
+  for (size_t j = 0; j < rem; ++j) out[4 * full + j] = g_decode_lut[packed[full]][j];
 }
 
 /* dot_ternary_i8_avx2 (simd.rs:118-171): sign-extend to i16, vpsignw,

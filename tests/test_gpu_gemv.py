@@ -146,3 +146,43 @@ def test_gemv_same_address_new_matrix(backend):
     w[:] = w2
     backend.ternary_gemv_preq(w, ws, act, aa, out, m, k)
     np.testing.assert_array_equal(out, ref(w, ws, act, aa, m, k))
+
+
+@pytest.mark.parametrize("shapes,k", [([2560, 640, 640], 2560), ([6912, 6912], 2560),
+                                      ([37, 0, 5, 16, 1, 3, 2, 100], 999)])
+def test_device_gemv_group_bit_exact(backend, shapes, k):
+    """One launch for matrices sharing the activation (q/k/v, gate/up),
+    including an empty matrix and a group of eight with odd sizes."""
+    case(f"ternary gemv group {shapes} k {k}")
+    import torch
+
+    rng = np.random.default_rng(len(shapes) * 1000 + k)
+    act = rng.integers(-128, 128, size=k).astype(np.int8)
+    aa = f32(7.5)
+    ws, dws, outs, refs, scales = [], [], [], [], []
+    for i, m in enumerate(shapes):
+        w, _, s_, _ = workload(3000 + 17 * i + k, m, k, garbage=0.02)
+        ws.append(w)
+        scales.append(s_)
+        dws.append(torch.from_numpy(w).cuda() if w.size else torch.zeros(16, dtype=torch.uint8, device="cuda"))
+        outs.append(torch.full((max(m, 1),), float("nan"), device="cuda"))
+        refs.append(ref(w, s_, act, aa, m, k))
+    backend.dev_ternary_gemv_preq_group(dws, scales, torch.from_numpy(act).cuda(), aa, outs,
+                                        shapes, k)
+    torch.cuda.synchronize()
+    for m, o, r in zip(shapes, outs, refs):
+        np.testing.assert_array_equal(o.cpu().numpy()[:m], r)
+
+
+def test_device_gemv_group_errors(backend):
+    case("ternary gemv group errors")
+    import bitnetrs_amd
+    import torch
+
+    a = torch.zeros(8, dtype=torch.int8, device="cuda")
+    w = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    o = torch.zeros(8, device="cuda")
+    with pytest.raises(bitnetrs_amd.InvalidConfig):
+        backend.dev_ternary_gemv_preq_group([w] * 9, [1.0] * 9, a, 1.0, [o] * 9, [8] * 9, 8)
+    with pytest.raises(bitnetrs_amd.QuantizationError, match="weight_scale must be finite > 0, got 0"):
+        backend.dev_ternary_gemv_preq_group([w, w], [1.0, 0.0], a, 1.0, [o, o], [8, 8], 8)
