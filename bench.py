@@ -344,6 +344,73 @@ def bench_gemv(torch, be, steps: int = 20, n_layers: int = 30):
             "gate_gbs": gate_bytes / (gate_us * 1e-6) / 1e9}
 
 
+LM_VOCAB, LM_HIDDEN = 128256, 2560  # BitNet b1.58 2B (LLaMA 3 tokenizer)
+
+
+def lm_head_bytes(v: int, h: int) -> int:
+    """i8 weights + f32 hidden in + f32 scales + f32 logits out."""
+    return v * h + 4 * h + 8 * v
+
+
+def bench_lm_head(torch, be, steps: int = 20):
+    """LM head with i8 weights at the 2B shape: 128256 x 2560 (328 MB, more
+    than the 256 MB MALL, so every launch streams it from HBM)."""
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7070)
+    w = torch.randint(-128, 128, (LM_VOCAB * LM_HIDDEN,), dtype=torch.int8, device="cuda",
+                      generator=g)
+    hid = torch.randn(LM_HIDDEN, device="cuda", generator=g)
+    sc = torch.rand(LM_VOCAB, device="cuda", generator=g) * 0.02
+    out = torch.zeros(LM_VOCAB, device="cuda")
+
+    def run():
+        be.dev_lm_head_matmul_i8(hid, w, sc, out, LM_VOCAB, LM_HIDDEN)
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            run()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    nbytes = lm_head_bytes(LM_VOCAB, LM_HIDDEN)
+    del w
+    torch.cuda.empty_cache()
+    return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
+
+
+def cpu_baseline_lm_head(budget_s: float):
+    """The oracle's lm_head_matmul_i8 (AVX2+FMA rows over all host cores) at
+    the 2B shape."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0xB17E7071)
+    w = rng.integers(-128, 128, size=LM_VOCAB * LM_HIDDEN, dtype=np.int8)
+    hid = rng.standard_normal(LM_HIDDEN).astype(np.float32)
+    sc = rng.uniform(0.0, 0.02, size=LM_VOCAB).astype(np.float32)
+    out = np.zeros(LM_VOCAB, np.float32)
+    n, t_start = 0, time.perf_counter()
+    while True:
+        oracle.lm_head_matmul_i8(hid, w, sc, out, LM_VOCAB, LM_HIDDEN)
+        n += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    dt = (time.perf_counter() - t_start) / n
+    return {"value": lm_head_bytes(LM_VOCAB, LM_HIDDEN) / dt / 1e9, "unit": "GB/s",
+            "cores": oracle.get_threads(), "kind": "port",
+            "sample": f"{n} x the 128256 x 2560 i8 LM head, {dt * 1e3:.2f} ms each"}
+
+
 def cpu_baseline_gemv(budget_s: float):
     """The oracle's ternary_gemv_preq (AVX2 integer dot, rows over all host
     cores) on the 7 projections of one layer for one token, repeated."""
@@ -456,6 +523,7 @@ def main() -> int:
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack workload")
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode")
     ap.add_argument("--no-gemv", action="store_true", help="skip the ternary GEMV workload")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the i8 LM head workload")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -560,6 +628,17 @@ def main() -> int:
                          "traffic": traffic.get("ternary_gemv_kernel", {}).get("bytes_per_launch"),
                          "kernel": "ternary_gemv_kernel (6912 x 2560)",
                          "kernel_us": round(gm["gate_us"], 3), "bytes_per_launch": gm["gate_bytes"]}}
+    if not args.no_lm_head:
+        lm = bench_lm_head(torch, be)
+        log(f"lm head i8 128256x2560: {lm['us']:.2f} us, {lm['gbs']:.0f} GB/s")
+        line["lm_head"] = {
+            "workload": "bitnet_2b_lm_head_i8_128256x2560",
+            "value": round(lm["gbs"], 2), "unit": "GB/s", "us_per_token": round(lm["us"], 3),
+            "roofline": {"bound": "hbm", "achieved": round(lm["gbs"], 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(lm["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("lm_head_i8_kernel", {}).get("bytes_per_launch"),
+                         "kernel": "lm_head_i8_kernel", "kernel_us": round(lm["us"], 3),
+                         "bytes_per_launch": lm["bytes"]}}
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)
@@ -567,6 +646,8 @@ def main() -> int:
             line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(args.cpu_budget)
         if not args.no_gemv:
             line["gemv"]["cpu_baseline"] = cpu_baseline_gemv(min(args.cpu_budget, 5.0))
+        if not args.no_lm_head:
+            line["lm_head"]["cpu_baseline"] = cpu_baseline_lm_head(min(args.cpu_budget, 5.0))
     be.close()
     print(json.dumps(line), flush=True)
     return 0

@@ -105,6 +105,9 @@ SIGNATURES = {
     "bnr_dev_ternary_gemv_preq_group": (_c.c_int, [_vp, _sz, _c.POINTER(_vp), _f, _vp,
                                                    _c.c_float, _c.POINTER(_vp),
                                                    _c.POINTER(_sz), _sz, _vp]),
+    "bnr_lm_head_matmul_i8_into": (_c.c_int, [_vp, _f, _sz, _vp, _sz, _f, _sz, _f, _sz, _sz,
+                                              _sz]),
+    "bnr_dev_lm_head_matmul_i8": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
 }
 

@@ -123,6 +123,16 @@ class HipBackend:
             weight_scale, _host_bytes(activation_q, np.int8, "activation_q"), activation_q.size,
             act_absmax, _host(output, "output"), output.size, out_features, in_features))
 
+    def lm_head_matmul_i8_into(self, hidden: np.ndarray, weights_i8: np.ndarray,
+                               scales: np.ndarray, output: np.ndarray, vocab_size: int,
+                               hidden_size: int) -> None:
+        """Backend::lm_head_matmul_i8_into (bitnet-core/src/backend/mod.rs:486-509)."""
+        _lib.check(self._L.bnr_lm_head_matmul_i8_into(
+            self._h, _host(hidden, "hidden"), hidden.size,
+            _host_bytes(weights_i8, np.int8, "weights_i8"), weights_i8.size,
+            _host(scales, "scales"), scales.size, _host(output, "output"), output.size,
+            vocab_size, hidden_size))
+
     def set_mirror_mode(self, mode: int) -> None:
         _lib.check(self._L.bnr_set_mirror_mode(self._h, mode))
 
@@ -196,6 +206,15 @@ class HipBackend:
         _lib.check(self._L.bnr_dev_ternary_gemv_preq_group(
             self._h, n, wp, sc, _dev(activation_q, "activation_q", dtype=torch.int8), act_absmax,
             op, mf, in_features, _stream(stream)))
+
+    def dev_lm_head_matmul_i8(self, hidden, weights_i8, scales, output, vocab_size, hidden_size,
+                              stream=None) -> None:
+        import torch
+
+        _lib.check(self._L.bnr_dev_lm_head_matmul_i8(
+            self._h, _dev(hidden, "hidden"), _dev(weights_i8, "weights_i8", dtype=torch.int8),
+            _dev(scales, "scales"), _dev(output, "output"), vocab_size, hidden_size,
+            _stream(stream)))
 
     def dev_synchronize(self, stream=None) -> None:
         _lib.check(self._L.bnr_dev_synchronize(self._h, _stream(stream)))

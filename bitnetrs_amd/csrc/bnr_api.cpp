@@ -866,6 +866,45 @@ int run_gemv(const uint8_t *w, float weight_scale, const int8_t *act, float act_
 
 }  // namespace
 
+// HBM copy of immutable host bytes (weights, scales), most recently used
+// first; *dev receives the device address.  Caller holds c->mu.
+int mirror_bytes(bnr_ctx *c, const void *host_p, size_t len, const uint8_t **dev) {
+  const uint8_t *host = (const uint8_t *)host_p;
+  uint8_t print[kFingerprint];
+  fingerprint(host, len, print);
+  auto it = c->weight_mirrors.begin();
+  for (; it != c->weight_mirrors.end(); ++it)
+    if (it->host == host && it->len == len) break;
+  if (it != c->weight_mirrors.end() && std::memcmp(it->print, print, kFingerprint) != 0) {
+    (void)hipStreamSynchronize(c->stream);  // different contents at the same address
+    (void)hipFree(it->dev);
+    c->weight_mirrors.erase(it);
+    it = c->weight_mirrors.end();
+  }
+  if (it != c->weight_mirrors.end()) {
+    c->weight_mirrors.splice(c->weight_mirrors.begin(), c->weight_mirrors, it);
+  } else {
+    if (c->weight_mirrors.size() >= kMaxWeightMirrors) {
+      (void)hipStreamSynchronize(c->stream);
+      (void)hipFree(c->weight_mirrors.back().dev);
+      c->weight_mirrors.pop_back();
+    }
+    WeightMirror m;
+    m.host = host;
+    m.len = len;
+    std::memcpy(m.print, print, kFingerprint);
+    HIP_TRY(hipMalloc((void **)&m.dev, len), "weight mirror alloc");
+    hipError_t e = hipMemcpyAsync(m.dev, host, len, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(m.dev);
+      return err_hip(e, "weight upload");
+    }
+    c->weight_mirrors.push_front(m);
+  }
+  *dev = c->weight_mirrors.front().dev;
+  return BNR_OK;
+}
+
 extern "C" int bnr_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed, size_t weight_len,
                                      float weight_scale, const int8_t *activation_q,
                                      size_t act_len, float act_absmax, float *output,
@@ -881,39 +920,8 @@ extern "C" int bnr_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed, s
   DeviceGuard dg(c->device);
   const uint8_t *dw = nullptr;
   if (weight_len) {
-    uint8_t print[kFingerprint];
-    fingerprint(weight_packed, weight_len, print);
-    auto it = c->weight_mirrors.begin();
-    for (; it != c->weight_mirrors.end(); ++it)
-      if (it->host == weight_packed && it->len == weight_len) break;
-    if (it != c->weight_mirrors.end() && std::memcmp(it->print, print, kFingerprint) != 0) {
-      (void)hipStreamSynchronize(c->stream);  // a different matrix at the same address
-      (void)hipFree(it->dev);
-      c->weight_mirrors.erase(it);
-      it = c->weight_mirrors.end();
-    }
-    if (it != c->weight_mirrors.end()) {
-      c->weight_mirrors.splice(c->weight_mirrors.begin(), c->weight_mirrors, it);
-    } else {
-      if (c->weight_mirrors.size() >= kMaxWeightMirrors) {
-        (void)hipStreamSynchronize(c->stream);
-        (void)hipFree(c->weight_mirrors.back().dev);
-        c->weight_mirrors.pop_back();
-      }
-      WeightMirror m;
-      m.host = weight_packed;
-      m.len = weight_len;
-      std::memcpy(m.print, print, kFingerprint);
-      HIP_TRY(hipMalloc((void **)&m.dev, weight_len), "weight mirror alloc");
-      hipError_t e = hipMemcpyAsync(m.dev, weight_packed, weight_len, hipMemcpyHostToDevice,
-                                    c->stream);
-      if (e != hipSuccess) {
-        (void)hipFree(m.dev);
-        return err_hip(e, "weight upload");
-      }
-      c->weight_mirrors.push_front(m);
-    }
-    dw = c->weight_mirrors.front().dev;
+    st = mirror_bytes(c, weight_packed, weight_len, &dw);
+    if (st) return st;
   }
   if (c->d_bytes_n < std::max<size_t>(in_features, 16)) {
     if (c->d_bytes) {
@@ -1239,6 +1247,95 @@ extern "C" int bnr_dev_prefill(bnr_ctx *c, float *q, float *k, const float *v, s
   if (st) return st;
   return bnr_dev_prefill_attention(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
                                    n_kv_heads, head_dim, stream);
+}
+
+// ---------------------------------------------------------------------------
+// LM head with i8 weights
+// ---------------------------------------------------------------------------
+namespace {
+
+int check_lm_head(size_t hidden_len, size_t weights_len, size_t scales_len, size_t out_len,
+                  size_t vocab_size, size_t hidden_size) {
+  if (hidden_len != SIZE_MAX && hidden_len != hidden_size)
+    return err_shape(fmt("hidden.len() == %zu", hidden_size), fmt("hidden.len() == %zu", hidden_len));
+  if (hidden_size != 0 && vocab_size > SIZE_MAX / hidden_size)
+    return err_shape("weight size fits usize", "overflow");
+  if (weights_len != SIZE_MAX && weights_len != vocab_size * hidden_size)
+    return err_shape(fmt("weights_i8.len() == %zu * %zu", vocab_size, hidden_size),
+                     fmt("weights_i8.len() == %zu", weights_len));
+  if (scales_len != SIZE_MAX && scales_len != vocab_size)
+    return err_shape(fmt("scales.len() == %zu", vocab_size), fmt("scales.len() == %zu", scales_len));
+  if (out_len != SIZE_MAX && out_len != vocab_size)
+    return err_shape(fmt("output.len() == %zu", vocab_size), fmt("output.len() == %zu", out_len));
+  if (hidden_size > (size_t)INT32_MAX)
+    return err_backend("lm_head_matmul_i8: hidden_size beyond 2^31 is not supported");
+  return BNR_OK;
+}
+
+int run_lm_head(const float *hidden, const int8_t *w, const float *scales, float *out,
+                size_t vocab_size, size_t hidden_size, hipStream_t s) {
+  LmHeadArgs a{};
+  a.hidden = hidden;
+  a.weight = w;
+  a.scales = scales;
+  a.out = out;
+  a.vocab_size = (long long)vocab_size;
+  a.hidden_size = (int)hidden_size;
+  const bool vec = hidden_size % 16 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)hidden % 16) == 0;
+  HIP_TRY(launch_lm_head_i8(a, vec, s), "lm_head launch");
+  return BNR_OK;
+}
+
+}  // namespace
+
+extern "C" int bnr_lm_head_matmul_i8_into(bnr_ctx *c, const float *hidden, size_t hidden_len,
+                                          const int8_t *weights_i8, size_t weights_len,
+                                          const float *scales, size_t scales_len, float *output,
+                                          size_t out_len, size_t vocab_size, size_t hidden_size) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_lm_head(hidden_len, weights_len, scales_len, out_len, vocab_size, hidden_size);
+  if (st) return st;
+  if (vocab_size == 0) return set_ok();
+  if ((hidden_size && (!hidden || !weights_i8)) || !scales || !output)
+    return err_backend("lm_head_matmul_i8_into: NULL slice");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  const uint8_t *dw = nullptr, *dsc = nullptr;
+  if (weights_len) {
+    st = mirror_bytes(c, weights_i8, weights_len, &dw);
+    if (st) return st;
+  }
+  st = mirror_bytes(c, scales, scales_len * sizeof(float), &dsc);
+  if (st) return st;
+  st = ensure_buf(&c->d_q, &c->d_q_n, std::max<size_t>(hidden_size, 4), "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_out, &c->d_out_n, vocab_size, "staging alloc");
+  if (st) return st;
+  if (hidden_size)
+    HIP_TRY(hipMemcpyAsync(c->d_q, hidden, hidden_size * 4, hipMemcpyHostToDevice, c->stream),
+            "upload hidden");
+  st = run_lm_head(c->d_q, (const int8_t *)dw, (const float *)dsc, c->d_out, vocab_size,
+                   hidden_size, c->stream);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(output, c->d_out, vocab_size * 4, hipMemcpyDeviceToHost, c->stream),
+          "download output");
+  HIP_TRY(hipStreamSynchronize(c->stream), "lm_head_matmul_i8_into");
+  return set_ok();
+}
+
+extern "C" int bnr_dev_lm_head_matmul_i8(bnr_ctx *c, const float *hidden, const int8_t *weights_i8,
+                                         const float *scales, float *output, size_t vocab_size,
+                                         size_t hidden_size, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_lm_head(SIZE_MAX, SIZE_MAX, SIZE_MAX, SIZE_MAX, vocab_size, hidden_size);
+  if (st) return st;
+  if (vocab_size == 0) return set_ok();
+  if ((hidden_size && (!hidden || !weights_i8)) || !scales || !output)
+    return err_backend("lm_head_matmul_i8: NULL pointer");
+  DeviceGuard dg(c->device);
+  st = run_lm_head(hidden, weights_i8, scales, output, vocab_size, hidden_size, (hipStream_t)stream);
+  if (st) return st;
+  return set_ok();
 }
 
 extern "C" int bnr_dev_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed,

@@ -186,3 +186,128 @@ hipError_t launch_ternary_gemv(const TernaryGemvArgs &a, bool vec, hipStream_t s
 }
 
 }  // namespace bnr
+
+// ---------------------------------------------------------------------------
+// LM head with i8 weights (CpuBackend::lm_head_matmul_i8_into,
+// bitnet-cpu/src/lib.rs:544-575): out[v] = (sum_k w[v][k] * h[k]) * scale[v],
+// w int8 [vocab x K], h f32 [K].  One HBM stream of vocab*K bytes (328 MB at
+// 128256 x 2560): a workgroup owns 128 rows (8 blocks of 16 rows, 16 lanes
+// per row, 16-byte pieces j, j+16, ... per lane) so that the hidden vector,
+// staged in LDS once per pass of 4096 values, is reused over 320 KB of
+// weights; the next block's pieces are loaded while the current block is
+// multiplied.  fp32 products and sums (any order; the reference's AVX2 lane
+// order is not reproduced, results agree to rounding).
+// ---------------------------------------------------------------------------
+namespace bnr {
+namespace {
+
+constexpr int kLmBlocks = 8;                     // row blocks of 16 per workgroup
+constexpr int kLmPass = 4096;                    // hidden values per LDS pass
+constexpr int kLmPieces = kLmPass / 16;          // 16-weight pieces per row and pass
+constexpr int kLmPiecesPerLane = kLmPieces / 16;
+
+__device__ __forceinline__ float row_sum16_f(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// acc += the 4 signed bytes of d times h.x .. h.w
+__device__ __forceinline__ float fma4_i8(unsigned d, float4 h, float acc) {
+  acc = fmaf((float)(int)(signed char)(d & 0xFF), h.x, acc);
+  acc = fmaf((float)(int)(signed char)((d >> 8) & 0xFF), h.y, acc);
+  acc = fmaf((float)(int)(signed char)((d >> 16) & 0xFF), h.z, acc);
+  acc = fmaf((float)((int)d >> 24), h.w, acc);
+  return acc;
+}
+
+// VEC: rows 16-byte aligned (K % 16 == 0, weights aligned).
+template <bool VEC>
+__global__ __launch_bounds__(256) void lm_head_i8_kernel(LmHeadArgs a) {
+  // hidden values 16c + 4t .. 16c + 4t + 3 of the pass at s_h[t * kLmPieces + c]
+  __shared__ float4 s_h[kLmPass / 4];
+  const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15;
+  const long long row0 = (long long)blockIdx.x * (16 * kLmBlocks) + slot;
+  float acc[kLmBlocks][2];
+#pragma unroll
+  for (int b = 0; b < kLmBlocks; ++b) acc[b][0] = acc[b][1] = 0.f;
+  for (int k0 = 0; k0 < a.hidden_size; k0 += kLmPass) {
+    const int kn = min(kLmPass, a.hidden_size - k0);
+    const int np = (kn + 15) / 16;  // pieces of the pass
+    __syncthreads();                // previous pass done with s_h
+    for (int g = tid; g < kLmPass / 4; g += 256) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int e = 4 * g;
+      if (e + 4 <= kn) {
+        v = *reinterpret_cast<const float4 *>(a.hidden + k0 + e);
+      } else if (e < kn) {
+        v.x = a.hidden[k0 + e];
+        if (e + 1 < kn) v.y = a.hidden[k0 + e + 1];
+        if (e + 2 < kn) v.z = a.hidden[k0 + e + 2];
+      }
+      s_h[(g & 3) * kLmPieces + (g >> 2)] = v;
+    }
+    __syncthreads();
+    auto load = [&](int b, uint4 *wv) {
+      const long long row = min(row0 + 16 * b, (long long)a.vocab_size - 1);
+      const int8_t *wr = a.weight + row * a.hidden_size + k0;
+#pragma unroll
+      for (int i = 0; i < kLmPiecesPerLane; ++i) {
+        const int c = j + 16 * i;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (c < np) {
+          if (VEC) {
+            v = *reinterpret_cast<const uint4 *>(wr + 16 * c);
+          } else {
+            unsigned d[4] = {0u, 0u, 0u, 0u};
+            for (int q = 0; q < 16; ++q)
+              if (16 * c + q < kn) d[q >> 2] |= (unsigned)(uint8_t)wr[16 * c + q] << (8 * (q & 3));
+            v = make_uint4(d[0], d[1], d[2], d[3]);
+          }
+        }
+        wv[i] = v;
+      }
+    };
+    uint4 wa[kLmPiecesPerLane], wb[kLmPiecesPerLane];
+    load(0, wa);
+#pragma unroll
+    for (int b = 0; b < kLmBlocks; ++b) {
+      uint4 *cur = (b & 1) ? wb : wa;
+      uint4 *nxt = (b & 1) ? wa : wb;
+      if (b + 1 < kLmBlocks) load(b + 1, nxt);
+#pragma unroll
+      for (int i = 0; i < kLmPiecesPerLane; ++i) {
+        const int c = j + 16 * i;
+        if (c < np) {
+          acc[b][0] = fma4_i8(cur[i].x, s_h[c], acc[b][0]);
+          acc[b][1] = fma4_i8(cur[i].y, s_h[kLmPieces + c], acc[b][1]);
+          acc[b][0] = fma4_i8(cur[i].z, s_h[2 * kLmPieces + c], acc[b][0]);
+          acc[b][1] = fma4_i8(cur[i].w, s_h[3 * kLmPieces + c], acc[b][1]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < kLmBlocks; ++b) {
+    const float s = row_sum16_f(acc[b][0] + acc[b][1]);
+    const long long row = row0 + 16 * b;
+    if (j == 0 && row < a.vocab_size) a.out[row] = s * a.scales[row];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_lm_head_i8(const LmHeadArgs &a, bool vec, hipStream_t s) {
+  if (a.vocab_size <= 0) return hipSuccess;
+  const long long rows_per_wg = 16 * kLmBlocks;
+  const dim3 grid((unsigned)((a.vocab_size + rows_per_wg - 1) / rows_per_wg));
+  if (vec)
+    lm_head_i8_kernel<true><<<grid, dim3(256), 0, s>>>(a);
+  else
+    lm_head_i8_kernel<false><<<grid, dim3(256), 0, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace bnr

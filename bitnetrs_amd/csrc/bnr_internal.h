@@ -130,4 +130,16 @@ struct TernaryGemvGroupArgs {
 };
 hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s);
 
+// LM head with i8 weights: out[v] = dot(weight[v], hidden) * scales[v].
+struct LmHeadArgs {
+  const float *hidden;
+  const int8_t *weight;   // [vocab_size x hidden_size]
+  const float *scales;    // [vocab_size]
+  float *out;             // [vocab_size]
+  long long vocab_size;
+  int hidden_size;
+};
+// vec: 16-byte aligned weights with hidden_size % 16 == 0, hidden 16-byte aligned.
+hipError_t launch_lm_head_i8(const LmHeadArgs &a, bool vec, hipStream_t s);
+
 }  // namespace bnr

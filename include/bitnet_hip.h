@@ -205,6 +205,24 @@ int bnr_dev_ternary_gemv_preq_group(bnr_ctx *ctx, size_t n, const uint8_t *const
                                     const size_t *out_features, size_t in_features,
                                     void *stream);
 
+/* Backend::lm_head_matmul_i8_into (bitnet-core/src/backend/mod.rs:470-509)
+ * as CpuBackend implements it (bitnet-cpu/src/lib.rs:544-575):
+ *   output[v] = (sum_h weights_i8[v*hidden_size + h] * hidden[h]) * scales[v]
+ * in fp32 (products and sums in an order of this library's choosing: the
+ * results agree with the reference's to rounding, not bit for bit).  Host
+ * slices, synchronous; weights and scales are mirrored in HBM as for
+ * bnr_ternary_gemv_preq.  Length mismatches (debug assertions in the
+ * reference) are InvalidShape. */
+int bnr_lm_head_matmul_i8_into(bnr_ctx *ctx, const float *hidden, size_t hidden_len,
+                               const int8_t *weights_i8, size_t weights_len, const float *scales,
+                               size_t scales_len, float *output, size_t out_len,
+                               size_t vocab_size, size_t hidden_size);
+/* The same on device pointers: hidden [hidden_size], weights_i8
+ * [vocab_size x hidden_size], scales and output [vocab_size]. */
+int bnr_dev_lm_head_matmul_i8(bnr_ctx *ctx, const float *hidden, const int8_t *weights_i8,
+                              const float *scales, float *output, size_t vocab_size,
+                              size_t hidden_size, void *stream);
+
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
 

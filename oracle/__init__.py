@@ -113,6 +113,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.bnro_dot_packed_ternary_i8.restype = ctypes.c_int32
     L.bnro_ternary_gemv_preq.argtypes = [_u8, _sz, ctypes.c_float, _u8, _sz, ctypes.c_float, _f,
                                          _sz, _sz, _sz]
+    L.bnro_dot_f32_i8w.argtypes = [_u8, _f, _sz]
+    L.bnro_dot_f32_i8w.restype = ctypes.c_float
+    L.bnro_lm_head_matmul_i8.argtypes = [_f, _sz, _u8, _sz, _f, _sz, _f, _sz, _sz, _sz]
 
 
 def _check(status: int) -> None:
@@ -329,3 +332,21 @@ def ternary_gemv_preq(weight_packed, weight_scale, activation_q, act_absmax, out
     _check(lib().bnro_ternary_gemv_preq(_bytes_ptr(w, np.uint8), w.size, weight_scale,
                                         _bytes_ptr(a, np.int8), a.size, act_absmax,
                                         _ptr(output), output.size, out_features, in_features))
+
+
+# ----------------------------------------------------------------------------
+# LM head with i8 weights
+# ----------------------------------------------------------------------------
+
+def dot_f32_i8w(w: np.ndarray, hidden: np.ndarray) -> float:
+    """simd::dot_f32_i8w_fast (bitnet-cpu/src/simd.rs:1255-1269)."""
+    w = np.ascontiguousarray(w, np.int8)
+    return float(lib().bnro_dot_f32_i8w(_bytes_ptr(w, np.int8), _ptr(hidden), w.size))
+
+
+def lm_head_matmul_i8(hidden, weights_i8, scales, output, vocab_size, hidden_size) -> None:
+    """CpuBackend::lm_head_matmul_i8_into (bitnet-cpu/src/lib.rs:544-575)."""
+    w = np.ascontiguousarray(weights_i8, np.int8).reshape(-1)
+    _check(lib().bnro_lm_head_matmul_i8(_ptr(hidden), hidden.size, _bytes_ptr(w, np.int8), w.size,
+                                        _ptr(scales), scales.size, _ptr(output), output.size,
+                                        vocab_size, hidden_size))

@@ -726,3 +726,67 @@ int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, floa
   }
   return ok();
 }
+
+/* ------------------------------------------------------------------------ */
+/* LM head with i8 weights                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* dot_f32_i8w_avx2 (simd.rs:1213-1246). */
+static float dot_i8w_avx2(const int8_t *w, const float *h, size_t n) {
+  const size_t chunks = n / 8, rem = n % 8;
+  __m256 acc = _mm256_setzero_ps();
+  for (size_t i = 0; i < chunks; ++i) {
+    const __m128i w8 = _mm_loadl_epi64((const __m128i *)(w + 8 * i));
+    const __m256 wf = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(w8));
+    acc = _mm256_fmadd_ps(wf, _mm256_loadu_ps(h + 8 * i), acc);
+  }
+  float r = hsum8(acc);
+  for (size_t i = 0; i < rem; ++i) r += (float)w[8 * chunks + i] * h[8 * chunks + i];
+  return r;
+}
+
+/* scalar fallback (simd.rs:1264-1268). */
+static float dot_i8w_scalar(const int8_t *w, const float *h, size_t n) {
+  float acc = 0.0f;
+  for (size_t i = 0; i < n; ++i) acc += (float)w[i] * h[i];
+  return acc;
+}
+
+float bnro_dot_f32_i8w(const int8_t *w, const float *hidden, size_t n) {
+  return use_avx2_fma() ? dot_i8w_avx2(w, hidden, n) : dot_i8w_scalar(w, hidden, n);
+}
+
+int bnro_lm_head_matmul_i8(const float *hidden, size_t hidden_len, const int8_t *weights,
+                           size_t weights_len, const float *scales, size_t scales_len,
+                           float *output, size_t out_len, size_t vocab_size,
+                           size_t hidden_size) {
+  char e[128], g[96];
+  if (hidden_len != hidden_size) {
+    snprintf(e, sizeof e, "hidden.len() == %zu", hidden_size);
+    snprintf(g, sizeof g, "hidden.len() == %zu", hidden_len);
+    return fail_shape(e, g);
+  }
+  if (hidden_size != 0 && vocab_size > SIZE_MAX / hidden_size)
+    return fail_shape("weight size fits usize", "overflow");
+  if (weights_len != vocab_size * hidden_size) {
+    snprintf(e, sizeof e, "weights_i8.len() == %zu * %zu", vocab_size, hidden_size);
+    snprintf(g, sizeof g, "weights_i8.len() == %zu", weights_len);
+    return fail_shape(e, g);
+  }
+  if (scales_len != vocab_size) {
+    snprintf(e, sizeof e, "scales.len() == %zu", vocab_size);
+    snprintf(g, sizeof g, "scales.len() == %zu", scales_len);
+    return fail_shape(e, g);
+  }
+  if (out_len != vocab_size) {
+    snprintf(e, sizeof e, "output.len() == %zu", vocab_size);
+    snprintf(g, sizeof g, "output.len() == %zu", out_len);
+    return fail_shape(e, g);
+  }
+  const int nthr = bnro_get_threads();
+  /* rayon par_chunks_mut(256): rows are independent, so any split is the same */
+#pragma omp parallel for num_threads(nthr) schedule(static, 256)
+  for (size_t v = 0; v < vocab_size; ++v)
+    output[v] = bnro_dot_f32_i8w(weights + v * hidden_size, hidden, hidden_size) * scales[v];
+  return ok();
+}

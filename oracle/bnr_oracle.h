@@ -125,6 +125,21 @@ int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, floa
                            float *output, size_t out_len, size_t out_features,
                            size_t in_features);
 
+/* ---- LM head with i8 weights ---- */
+
+/* simd::dot_f32_i8w_fast  bitnet-cpu/src/simd.rs:1255-1269 (AVX2+FMA body
+ * dot_f32_i8w_avx2 1213-1246: 8 lanes, i8 -> f32, fmadd per 8-chunk,
+ * hsum_f32_avx2 292-307, unfused scalar tail; scalar fallback 1264-1268). */
+float bnro_dot_f32_i8w(const int8_t *w, const float *hidden, size_t n);
+/* CpuBackend::lm_head_matmul_i8_into  bitnet-cpu/src/lib.rs:544-575:
+ * output[v] = dot_f32_i8w(weights[v*hidden_size ..], hidden) * scales[v].
+ * The reference only debug-asserts the lengths; here a mismatch is
+ * InvalidShape. */
+int bnro_lm_head_matmul_i8(const float *hidden, size_t hidden_len, const int8_t *weights,
+                           size_t weights_len, const float *scales, size_t scales_len,
+                           float *output, size_t out_len, size_t vocab_size,
+                           size_t hidden_size);
+
 /* Number of OpenMP threads the attention head loop uses (Rayon sizes its
  * pool to all logical cores, lib.rs:99-133). 0 = all cores. */
 void bnro_set_threads(int n);
