@@ -25,6 +25,10 @@ BNR_QUANTIZATION_ERROR = 5
 BNR_MIRROR_INCREMENTAL = 0
 BNR_MIRROR_FULL = 1
 
+BNR_GLUE_PLAIN = 0
+BNR_GLUE_RESIDUAL = 1
+BNR_GLUE_SQRELU = 2
+
 
 class BitNetError(Exception):
     """Mirror of bitnet_core::error::BitNetError (bitnet-core/src/error.rs:12-55)."""
@@ -108,6 +112,17 @@ SIGNATURES = {
     "bnr_lm_head_matmul_i8_into": (_c.c_int, [_vp, _f, _sz, _vp, _sz, _f, _sz, _f, _sz, _sz,
                                               _sz]),
     "bnr_dev_lm_head_matmul_i8": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _vp]),
+    "bnr_dev_ternary_gemv_preq_group_devscale": (_c.c_int, [_vp, _sz, _c.POINTER(_vp), _f, _vp,
+                                                            _vp, _c.POINTER(_vp),
+                                                            _c.POINTER(_sz), _sz, _vp]),
+    "bnr_rms_norm": (_c.c_int, [_vp, _f, _sz, _f, _sz, _c.c_float, _f, _sz]),
+    "bnr_sqrelu_gate": (_c.c_int, [_vp, _f, _sz, _f, _sz, _f, _sz]),
+    "bnr_dev_rms_norm": (_c.c_int, [_vp, _vp, _vp, _c.c_float, _vp, _sz, _vp]),
+    "bnr_dev_sqrelu_gate": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp]),
+    "bnr_dev_residual_add": (_c.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "bnr_dev_absmax_quantize": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp]),
+    "bnr_dev_norm_quant": (_c.c_int, [_vp, _c.c_int, _vp, _vp, _vp, _c.c_float, _sz, _vp, _vp,
+                                      _vp, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
 }
 

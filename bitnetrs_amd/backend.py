@@ -133,6 +133,18 @@ class HipBackend:
             _host(scales, "scales"), scales.size, _host(output, "output"), output.size,
             vocab_size, hidden_size))
 
+    def rms_norm(self, input: np.ndarray, weight: np.ndarray, eps: float,
+                 output: np.ndarray) -> None:
+        """Backend::rms_norm (CpuBackend: bitnet-cpu/src/norm.rs:76-136)."""
+        _lib.check(self._L.bnr_rms_norm(self._h, _host(input, "input"), input.size,
+                                        _host(weight, "weight"), weight.size, eps,
+                                        _host(output, "output"), output.size))
+
+    def sqrelu_gate(self, gate: np.ndarray, up: np.ndarray, out: np.ndarray) -> None:
+        """Backend::sqrelu_gate (CpuBackend: bitnet-cpu/src/lib.rs:494-509)."""
+        _lib.check(self._L.bnr_sqrelu_gate(self._h, _host(gate, "gate"), gate.size,
+                                           _host(up, "up"), up.size, _host(out, "out"), out.size))
+
     def set_mirror_mode(self, mode: int) -> None:
         _lib.check(self._L.bnr_set_mirror_mode(self._h, mode))
 
@@ -215,6 +227,51 @@ class HipBackend:
             self._h, _dev(hidden, "hidden"), _dev(weights_i8, "weights_i8", dtype=torch.int8),
             _dev(scales, "scales"), _dev(output, "output"), vocab_size, hidden_size,
             _stream(stream)))
+
+    def dev_ternary_gemv_preq_group_devscale(self, weights, weight_scales, activation_q,
+                                             act_absmax, outputs, out_features, in_features,
+                                             stream=None) -> None:
+        """Grouped ternary GEMV with the activation scale in device memory."""
+        import torch
+
+        n = len(weights)
+        wp = (ctypes.c_void_p * n)(*[_dev(w, "weight", dtype=torch.uint8).value for w in weights])
+        op = (ctypes.c_void_p * n)(*[_dev(o, "output").value for o in outputs])
+        sc = (ctypes.c_float * n)(*[float(x) for x in weight_scales])
+        mf = (ctypes.c_size_t * n)(*[int(x) for x in out_features])
+        _lib.check(self._L.bnr_dev_ternary_gemv_preq_group_devscale(
+            self._h, n, wp, sc, _dev(activation_q, "activation_q", dtype=torch.int8),
+            _dev(act_absmax, "act_absmax"), op, mf, in_features, _stream(stream)))
+
+    def dev_rms_norm(self, input, weight, eps, output, n, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_rms_norm(self._h, _dev(input, "input"), _dev(weight, "weight"),
+                                            eps, _dev(output, "output"), n, _stream(stream)))
+
+    def dev_sqrelu_gate(self, gate, up, out, n, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_sqrelu_gate(self._h, _dev(gate, "gate"), _dev(up, "up"),
+                                               _dev(out, "out"), n, _stream(stream)))
+
+    def dev_residual_add(self, h, delta, n, stream=None) -> None:
+        _lib.check(self._L.bnr_dev_residual_add(self._h, _dev(h, "h"), _dev(delta, "delta"), n,
+                                                _stream(stream)))
+
+    def dev_absmax_quantize(self, x, q_out, scale_out, n, stream=None) -> None:
+        import torch
+
+        _lib.check(self._L.bnr_dev_absmax_quantize(
+            self._h, _dev(x, "x"), _dev(q_out, "q_out", dtype=torch.int8),
+            _dev(scale_out, "scale_out"), n, _stream(stream)))
+
+    def dev_norm_quant(self, mode, a, b, gamma, eps, n, h_out, q_out, act_absmax,
+                       stream=None) -> None:
+        """x = a | a + b (-> h_out) | sqrelu(a) * b; RMSNorm with gamma; int8
+        absmax quantisation into q_out with act_absmax (device float)."""
+        import torch
+
+        _lib.check(self._L.bnr_dev_norm_quant(
+            self._h, int(mode), _dev(a, "a"), _dev(b, "b", True), _dev(gamma, "gamma"), eps, n,
+            _dev(h_out, "h_out", True), _dev(q_out, "q_out", dtype=torch.int8),
+            _dev(act_absmax, "act_absmax"), _stream(stream)))
 
     def dev_synchronize(self, stream=None) -> None:
         _lib.check(self._L.bnr_dev_synchronize(self._h, _stream(stream)))

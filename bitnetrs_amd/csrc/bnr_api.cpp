@@ -1356,12 +1356,14 @@ extern "C" int bnr_dev_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packe
   return set_ok();
 }
 
-extern "C" int bnr_dev_ternary_gemv_preq_group(bnr_ctx *c, size_t n,
-                                               const uint8_t *const *weight_packed,
-                                               const float *weight_scales,
-                                               const int8_t *activation_q, float act_absmax,
-                                               float *const *outputs, const size_t *out_features,
-                                               size_t in_features, void *stream) {
+namespace {
+
+// Grouped GEMV launch; act_absmax_dev non-null: the activation scale is read
+// from device memory (produced by the fused norm/quantise kernel).
+int run_gemv_group(bnr_ctx *c, size_t n, const uint8_t *const *weight_packed,
+                   const float *weight_scales, const int8_t *activation_q, float act_absmax,
+                   const float *act_absmax_dev, float *const *outputs,
+                   const size_t *out_features, size_t in_features, hipStream_t stream) {
   if (!c) return err_backend("context is NULL");
   if (n == 0 || n > (size_t)kMaxGemvGroup)
     return err_config(fmt("ternary GEMV group size must be 1..%d, got %zu", kMaxGemvGroup, n));
@@ -1372,16 +1374,18 @@ extern "C" int bnr_dev_ternary_gemv_preq_group(bnr_ctx *c, size_t n,
   g.act = activation_q;
   g.in_features = (int)in_features;
   g.packed_cols = (long long)((in_features + 3) / 4);
+  g.act_absmax_dev = act_absmax_dev;
   bool vec = g.packed_cols % 16 == 0 && ((uintptr_t)activation_q % 16) == 0;
   int wgs = 0;
   for (size_t i = 0; i < n; ++i) {
-    int st = check_gemv(SIZE_MAX, weight_scales[i], SIZE_MAX, act_absmax, SIZE_MAX,
-                        out_features[i], in_features);
+    int st = check_gemv(SIZE_MAX, weight_scales[i], SIZE_MAX, act_absmax_dev ? 1.0f : act_absmax,
+                        SIZE_MAX, out_features[i], in_features);
     if (st) return st;
     if (out_features[i] && ((in_features && (!weight_packed[i] || !activation_q)) || !outputs[i]))
       return err_backend("ternary_gemv_preq_group: NULL pointer");
     g.weight[i] = weight_packed[i];
     g.out[i] = outputs[i];
+    g.weight_scale[i] = weight_scales[i];
     volatile float ws_as = weight_scales[i] * act_absmax;
     g.scale[i] = ws_as / 127.0f;
     g.out_features[i] = (int)out_features[i];
@@ -1392,8 +1396,175 @@ extern "C" int bnr_dev_ternary_gemv_preq_group(bnr_ctx *c, size_t n,
   for (size_t i = n; i <= (size_t)kMaxGemvGroup; ++i) g.wg_off[i] = wgs;
   if (wgs == 0) return set_ok();
   DeviceGuard dg(c->device);
-  HIP_TRY(launch_ternary_gemv_group(g, vec, (hipStream_t)stream), "ternary_gemv group launch");
+  HIP_TRY(launch_ternary_gemv_group(g, vec, stream), "ternary_gemv group launch");
   return set_ok();
+}
+
+}  // namespace
+
+extern "C" int bnr_dev_ternary_gemv_preq_group(bnr_ctx *c, size_t n,
+                                               const uint8_t *const *weight_packed,
+                                               const float *weight_scales,
+                                               const int8_t *activation_q, float act_absmax,
+                                               float *const *outputs, const size_t *out_features,
+                                               size_t in_features, void *stream) {
+  return run_gemv_group(c, n, weight_packed, weight_scales, activation_q, act_absmax, nullptr,
+                        outputs, out_features, in_features, (hipStream_t)stream);
+}
+
+extern "C" int bnr_dev_ternary_gemv_preq_group_devscale(
+    bnr_ctx *c, size_t n, const uint8_t *const *weight_packed, const float *weight_scales,
+    const int8_t *activation_q, const float *act_absmax, float *const *outputs,
+    const size_t *out_features, size_t in_features, void *stream) {
+  if (!act_absmax) return err_backend("ternary_gemv_preq_group_devscale: NULL act_absmax");
+  return run_gemv_group(c, n, weight_packed, weight_scales, activation_q, 1.0f, act_absmax,
+                        outputs, out_features, in_features, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Layer glue
+// ---------------------------------------------------------------------------
+namespace {
+
+// norm::rms_norm checks (bitnet-cpu/src/norm.rs:77-97), in its order.
+int check_rms_norm(size_t in_len, size_t w_len, float eps, size_t out_len) {
+  if (in_len != w_len)
+    return err_shape(fmt("input.len() == weight.len() = %zu", w_len), fmt("input.len() = %zu", in_len));
+  if (in_len != out_len)
+    return err_shape(fmt("input.len() == output.len() = %zu", in_len), fmt("output.len() = %zu", out_len));
+  if (eps <= 0.0f || !std::isfinite(eps))
+    return err_quant("eps must be finite and > 0, got " + rust_f32(eps));
+  if (in_len > (size_t)INT32_MAX) return err_backend("rms_norm: length beyond 2^31 is not supported");
+  return BNR_OK;
+}
+
+int run_norm_quant(bnr_ctx *c, int mode, const float *a, const float *b, const float *gamma,
+                   float eps, size_t n, float *h_out, float *y_out, int8_t *q_out,
+                   float *scale_out, float *act_absmax, hipStream_t s) {
+  NormQuantArgs na{};
+  na.mode = mode;
+  na.a = a;
+  na.b = b;
+  na.gamma = gamma;
+  na.eps = eps;
+  na.n = (int)n;
+  na.h_out = h_out;
+  na.y_out = y_out;
+  na.q_out = q_out;
+  na.scale_out = scale_out;
+  na.act_absmax = act_absmax;
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_norm_quant(na, s), "norm_quant launch");
+  return BNR_OK;
+}
+
+}  // namespace
+
+extern "C" int bnr_rms_norm(bnr_ctx *c, const float *input, size_t in_len, const float *weight,
+                            size_t w_len, float eps, float *output, size_t out_len) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_rms_norm(in_len, w_len, eps, out_len);
+  if (st) return st;
+  if (in_len == 0) return set_ok();
+  if (!input || !weight || !output) return err_backend("rms_norm: NULL slice");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  const uint8_t *dw = nullptr;
+  st = mirror_bytes(c, weight, w_len * sizeof(float), &dw);
+  if (st) return st;
+  st = ensure_buf(&c->d_q, &c->d_q_n, in_len, "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_out, &c->d_out_n, in_len, "staging alloc");
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(c->d_q, input, in_len * 4, hipMemcpyHostToDevice, c->stream), "upload input");
+  st = run_norm_quant(c, kGluePlain, c->d_q, nullptr, (const float *)dw, eps, in_len, nullptr,
+                      c->d_out, nullptr, nullptr, nullptr, c->stream);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(output, c->d_out, in_len * 4, hipMemcpyDeviceToHost, c->stream), "download output");
+  HIP_TRY(hipStreamSynchronize(c->stream), "rms_norm");
+  return set_ok();
+}
+
+extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, const float *up,
+                               size_t u_len, float *out, size_t out_len) {
+  if (!c) return err_backend("context is NULL");
+  if (g_len != u_len || g_len != out_len)
+    return err_shape(fmt("gate.len() == up.len() == out.len() = %zu", g_len),
+                     fmt("up.len()=%zu, out.len()=%zu", u_len, out_len));
+  if (g_len == 0) return set_ok();
+  if (!gate || !up || !out) return err_backend("sqrelu_gate: NULL slice");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  int st = ensure_buf(&c->d_q, &c->d_q_n, 2 * g_len, "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_out, &c->d_out_n, g_len, "staging alloc");
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(c->d_q, gate, g_len * 4, hipMemcpyHostToDevice, c->stream), "upload gate");
+  HIP_TRY(hipMemcpyAsync(c->d_q + g_len, up, g_len * 4, hipMemcpyHostToDevice, c->stream), "upload up");
+  HIP_TRY(launch_sqrelu(c->d_q, c->d_q + g_len, c->d_out, (long long)g_len, c->stream), "sqrelu launch");
+  HIP_TRY(hipMemcpyAsync(out, c->d_out, g_len * 4, hipMemcpyDeviceToHost, c->stream), "download out");
+  HIP_TRY(hipStreamSynchronize(c->stream), "sqrelu_gate");
+  return set_ok();
+}
+
+extern "C" int bnr_dev_rms_norm(bnr_ctx *c, const float *input, const float *weight, float eps,
+                                float *output, size_t n, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_rms_norm(n, n, eps, n);
+  if (st) return st;
+  if (n == 0) return set_ok();
+  if (!input || !weight || !output) return err_backend("rms_norm: NULL pointer");
+  st = run_norm_quant(c, kGluePlain, input, nullptr, weight, eps, n, nullptr, output, nullptr,
+                      nullptr, nullptr, (hipStream_t)stream);
+  return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_sqrelu_gate(bnr_ctx *c, const float *gate, const float *up, float *out,
+                                   size_t n, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (n == 0) return set_ok();
+  if (!gate || !up || !out) return err_backend("sqrelu_gate: NULL pointer");
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_sqrelu(gate, up, out, (long long)n, (hipStream_t)stream), "sqrelu launch");
+  return set_ok();
+}
+
+extern "C" int bnr_dev_residual_add(bnr_ctx *c, float *h, const float *delta, size_t n,
+                                    void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (n == 0) return set_ok();
+  if (!h || !delta) return err_backend("residual_add: NULL pointer");
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_residual(h, delta, (long long)n, (hipStream_t)stream), "residual launch");
+  return set_ok();
+}
+
+extern "C" int bnr_dev_absmax_quantize(bnr_ctx *c, const float *x, int8_t *q_out, float *scale_out,
+                                       size_t n, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (n == 0) return err_quant("cannot quantise an empty activation vector");
+  if (n > (size_t)INT32_MAX) return err_backend("absmax_quantize: length beyond 2^31 is not supported");
+  if (!x || !q_out || !scale_out) return err_backend("absmax_quantize: NULL pointer");
+  int st = run_norm_quant(c, kGluePlain, x, nullptr, nullptr, 1.0f, n, nullptr, nullptr, q_out,
+                          scale_out, nullptr, (hipStream_t)stream);
+  return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_norm_quant(bnr_ctx *c, int mode, const float *a, const float *b,
+                                  const float *gamma, float eps, size_t n, float *h_out,
+                                  int8_t *q_out, float *act_absmax, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (mode != BNR_GLUE_PLAIN && mode != BNR_GLUE_RESIDUAL && mode != BNR_GLUE_SQRELU)
+    return err_config(fmt("unknown norm_quant mode %d", mode));
+  int st = check_rms_norm(n, n, eps, n);
+  if (st) return st;
+  if (n == 0) return err_quant("cannot quantise an empty activation vector");
+  if (!a || !gamma || !q_out || !act_absmax || (mode != BNR_GLUE_PLAIN && !b) ||
+      (mode == BNR_GLUE_RESIDUAL && !h_out))
+    return err_backend("norm_quant: NULL pointer");
+  st = run_norm_quant(c, mode, a, b, gamma, eps, n, mode == BNR_GLUE_RESIDUAL ? h_out : nullptr,
+                      nullptr, q_out, nullptr, act_absmax, (hipStream_t)stream);
+  return st ? st : set_ok();
 }
 
 extern "C" int bnr_dev_synchronize(bnr_ctx *c, void *stream) {

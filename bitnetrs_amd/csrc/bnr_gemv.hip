@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
   // argument arrays stay in scalar registers.
   const uint8_t *w = a.weight[0];
   float *out = a.out[0];
-  float scale = a.scale[0];
+  float scale = a.scale[0], ws = a.weight_scale[0];
   int m = a.out_features[0], off = 0;
 #pragma unroll
   for (int i = 1; i < kMaxGemvGroup; ++i) {
@@ -156,9 +156,15 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
       w = a.weight[i];
       out = a.out[i];
       scale = a.scale[i];
+      ws = a.weight_scale[i];
       m = a.out_features[i];
       off = a.wg_off[i];
     }
+  }
+  if (a.act_absmax_dev) {
+    // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), f32, left to right
+    const float t = ws * *a.act_absmax_dev;
+    scale = t / 127.0f;
   }
   gemv_rows<VEC>(w, a.act, out, m, a.in_features, a.packed_cols, scale, b - off, s_act);
 }

@@ -127,6 +127,10 @@ struct TernaryGemvGroupArgs {
   const int8_t *act;
   long long packed_cols;
   int in_features, n;
+  // When non-null, act_absmax is read from device memory and scale[i] is
+  // formed in the kernel as (weight_scale[i] * act_absmax) / 127.
+  const float *act_absmax_dev;
+  float weight_scale[kMaxGemvGroup];
 };
 hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s);
 
@@ -141,5 +145,25 @@ struct LmHeadArgs {
 };
 // vec: 16-byte aligned weights with hidden_size % 16 == 0, hidden 16-byte aligned.
 hipError_t launch_lm_head_i8(const LmHeadArgs &a, bool vec, hipStream_t s);
+
+// Layer glue (bnr_glue.hip).
+constexpr int kGluePlain = 0;     // x = a
+constexpr int kGlueResidual = 1;  // x = a + b, written to h_out
+constexpr int kGlueSqrelu = 2;    // x = max(a, 0)^2 * b
+struct NormQuantArgs {
+  int mode;
+  const float *a, *b;
+  const float *gamma;   // RMSNorm weight, or null: no normalisation
+  float eps;
+  int n;
+  float *h_out;         // mode kGlueResidual: a + b (may alias a)
+  float *y_out;         // optional: normalised values
+  int8_t *q_out;        // optional: absmax int8 quantisation of y
+  float *scale_out;     // optional (with q_out): max|y| / 127
+  float *act_absmax;    // optional (with q_out): scale * 127, what the projections take
+};
+hipError_t launch_norm_quant(const NormQuantArgs &a, hipStream_t s);
+hipError_t launch_sqrelu(const float *gate, const float *up, float *out, long long n, hipStream_t s);
+hipError_t launch_residual(float *h, const float *delta, long long n, hipStream_t s);
 
 }  // namespace bnr

@@ -223,6 +223,62 @@ int bnr_dev_lm_head_matmul_i8(bnr_ctx *ctx, const float *hidden, const int8_t *w
                               const float *scales, float *output, size_t vocab_size,
                               size_t hidden_size, void *stream);
 
+/* bnr_dev_ternary_gemv_preq_group with the activation scale act_absmax read
+ * from device memory (one float, as written by bnr_dev_norm_quant), so that
+ * a decode layer runs without a host round trip. */
+int bnr_dev_ternary_gemv_preq_group_devscale(bnr_ctx *ctx, size_t n,
+                                             const uint8_t *const *weight_packed,
+                                             const float *weight_scales,
+                                             const int8_t *activation_q, const float *act_absmax,
+                                             float *const *outputs, const size_t *out_features,
+                                             size_t in_features, void *stream);
+
+/* ---- Layer glue ----------------------------------------------------------- */
+
+/* Backend::rms_norm (bitnet-core/src/backend/mod.rs) as CpuBackend implements
+ * it (bitnet-cpu/src/lib.rs:268-270 -> norm::rms_norm, norm.rs:76-136):
+ * out[i] = x[i] * (1/sqrt(sum(x^2)/n + eps)) * weight[i].  The sum of squares
+ * is reduced as a tree, so outputs agree with the reference's to rounding.
+ * Host slices, synchronous; the weight is mirrored in HBM.  Checks and
+ * messages as norm.rs:77-97 (InvalidShape, QuantizationError for eps). */
+int bnr_rms_norm(bnr_ctx *ctx, const float *input, size_t in_len, const float *weight,
+                 size_t w_len, float eps, float *output, size_t out_len);
+/* Backend::sqrelu_gate as CpuBackend implements it (bitnet-cpu/src/lib.rs:
+ * 494-509): out[i] = max(gate[i], 0)^2 * up[i], bit-identical.  Host slices. */
+int bnr_sqrelu_gate(bnr_ctx *ctx, const float *gate, size_t g_len, const float *up,
+                    size_t u_len, float *out, size_t out_len);
+/* Device forms of the two (n elements each). */
+int bnr_dev_rms_norm(bnr_ctx *ctx, const float *input, const float *weight, float eps,
+                     float *output, size_t n, void *stream);
+int bnr_dev_sqrelu_gate(bnr_ctx *ctx, const float *gate, const float *up, float *out, size_t n,
+                        void *stream);
+/* h[i] += delta[i]: the residual axpy_f32_fast(1.0, delta, h) of
+ * BitNetModel::forward (bitnet-model/src/lib.rs:1061,1130), bit-identical. */
+int bnr_dev_residual_add(bnr_ctx *ctx, float *h, const float *delta, size_t n, void *stream);
+/* absmax_quantize_row_into (bitnet-core/src/quant/absmax.rs:127-170) on
+ * device: q_out [n] int8 and *scale_out (device) = max(max|x|, 1e-5) / 127,
+ * bit-identical.  Finite inputs are assumed (the reference's non-finite
+ * check is not repeated on the device). */
+int bnr_dev_absmax_quantize(bnr_ctx *ctx, const float *x, int8_t *q_out, float *scale_out,
+                            size_t n, void *stream);
+
+/* One launch between two projections of a decode layer: form x, RMSNorm it
+ * with gamma, quantise the result (absmax int8) for the next ternary GEMV.
+ *   BNR_GLUE_PLAIN    x = a                                   (attention and
+ *                     sub-norms, bitnet-model/src/lib.rs:628-642, 720-730)
+ *   BNR_GLUE_RESIDUAL x = a + b, written to h_out (may be a)  (residual then
+ *                     ffn_norm, lib.rs:743-759)
+ *   BNR_GLUE_SQRELU   x = max(a,0)^2 * b                      (sqrelu_gate then
+ *                     ffn_sub_norm, lib.rs:788-800)
+ * q_out [n] int8; *act_absmax (device) = (max|y| / 127) * 127, the value the
+ * model passes to ternary_gemv_preq (lib.rs:642). */
+#define BNR_GLUE_PLAIN 0
+#define BNR_GLUE_RESIDUAL 1
+#define BNR_GLUE_SQRELU 2
+int bnr_dev_norm_quant(bnr_ctx *ctx, int mode, const float *a, const float *b, const float *gamma,
+                       float eps, size_t n, float *h_out, int8_t *q_out, float *act_absmax,
+                       void *stream);
+
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
 

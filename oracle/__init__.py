@@ -116,6 +116,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.bnro_dot_f32_i8w.argtypes = [_u8, _f, _sz]
     L.bnro_dot_f32_i8w.restype = ctypes.c_float
     L.bnro_lm_head_matmul_i8.argtypes = [_f, _sz, _u8, _sz, _f, _sz, _f, _sz, _sz, _sz]
+    L.bnro_sum_squares_f32.argtypes = [_f, _sz]
+    L.bnro_sum_squares_f32.restype = ctypes.c_float
+    L.bnro_rms_norm.argtypes = [_f, _sz, _f, _sz, ctypes.c_float, _f, _sz]
+    L.bnro_absmax_quantize_row.argtypes = [_f, _sz, _u8, _sz, ctypes.POINTER(ctypes.c_float)]
+    L.bnro_sqrelu_gate.argtypes = [_f, _sz, _f, _sz, _f, _sz]
 
 
 def _check(status: int) -> None:
@@ -350,3 +355,33 @@ def lm_head_matmul_i8(hidden, weights_i8, scales, output, vocab_size, hidden_siz
     _check(lib().bnro_lm_head_matmul_i8(_ptr(hidden), hidden.size, _bytes_ptr(w, np.int8), w.size,
                                         _ptr(scales), scales.size, _ptr(output), output.size,
                                         vocab_size, hidden_size))
+
+
+# ----------------------------------------------------------------------------
+# Layer glue
+# ----------------------------------------------------------------------------
+
+def sum_squares(x: np.ndarray) -> float:
+    return float(lib().bnro_sum_squares_f32(_ptr(x), x.size))
+
+
+def rms_norm(input, weight, eps, output) -> None:
+    """norm::rms_norm (bitnet-cpu/src/norm.rs:76-136)."""
+    _check(lib().bnro_rms_norm(_ptr(input), input.size, _ptr(weight), weight.size, eps,
+                               _ptr(output), output.size))
+
+
+def absmax_quantize_row(x: np.ndarray, out: np.ndarray = None):
+    """absmax_quantize_row_into (bitnet-core/src/quant/absmax.rs:127-170);
+    returns (q, scale) with scale = max|x| / 127."""
+    if out is None:
+        out = np.zeros(x.size, np.int8)
+    sc = ctypes.c_float()
+    _check(lib().bnro_absmax_quantize_row(_ptr(x), x.size, _bytes_ptr(out, np.int8), out.size,
+                                          ctypes.byref(sc)))
+    return out, float(np.float32(sc.value))
+
+
+def sqrelu_gate(gate, up, out) -> None:
+    """CpuBackend::sqrelu_gate (bitnet-cpu/src/lib.rs:494-509)."""
+    _check(lib().bnro_sqrelu_gate(_ptr(gate), gate.size, _ptr(up), up.size, _ptr(out), out.size))

@@ -790,3 +790,100 @@ int bnro_lm_head_matmul_i8(const float *hidden, size_t hidden_len, const int8_t 
     output[v] = bnro_dot_f32_i8w(weights + v * hidden_size, hidden, hidden_size) * scales[v];
   return ok();
 }
+
+/* ------------------------------------------------------------------------ */
+/* Layer glue: RMSNorm, absmax quantisation, squared-ReLU gate               */
+/* ------------------------------------------------------------------------ */
+
+/* sum_squares_f32_avx2 (simd.rs:802-828) and the scalar fallback (simd.rs:838). */
+float bnro_sum_squares_f32(const float *x, size_t n) {
+  if (use_avx2_fma()) {
+    const size_t chunks = n / 8, rem = n % 8;
+    __m256 acc = _mm256_setzero_ps();
+    for (size_t i = 0; i < chunks; ++i) {
+      const __m256 v = _mm256_loadu_ps(x + 8 * i);
+      acc = _mm256_fmadd_ps(v, v, acc);
+    }
+    float r = hsum8(acc);
+    for (size_t i = 0; i < rem; ++i) r += x[8 * chunks + i] * x[8 * chunks + i];
+    return r;
+  }
+  float acc = 0.0f;
+  for (size_t i = 0; i < n; ++i) acc += x[i] * x[i];
+  return acc;
+}
+
+/* norm.rs:76-136 */
+int bnro_rms_norm(const float *input, size_t in_len, const float *weight, size_t w_len,
+                  float eps, float *output, size_t out_len) {
+  char e[96], g[96], f[64];
+  if (in_len != w_len) {
+    snprintf(e, sizeof e, "input.len() == weight.len() = %zu", w_len);
+    snprintf(g, sizeof g, "input.len() = %zu", in_len);
+    return fail_shape(e, g);
+  }
+  if (in_len != out_len) {
+    snprintf(e, sizeof e, "input.len() == output.len() = %zu", in_len);
+    snprintf(g, sizeof g, "output.len() = %zu", out_len);
+    return fail_shape(e, g);
+  }
+  if (eps <= 0.0f || !isfinite(eps)) {
+    rust_f32(f, sizeof f, eps);
+    snprintf(e, sizeof e, "eps must be finite and > 0, got %s", f);
+    return fail_quant(e);
+  }
+  if (in_len == 0) return ok();
+  const float d = (float)in_len;
+  const float sum_sq = bnro_sum_squares_f32(input, in_len);
+  const float rms = sqrtf(sum_sq / d + eps);
+  const float inv = 1.0f / rms;
+  for (size_t i = 0; i < in_len; ++i) output[i] = input[i] * inv * weight[i];
+  return ok();
+}
+
+/* absmax.rs:127-170 */
+int bnro_absmax_quantize_row(const float *x, size_t n, int8_t *out, size_t out_len,
+                             float *scale) {
+  char e[128], f[64];
+  if (n == 0) return fail_quant("cannot quantise an empty activation vector");
+  if (out_len != n) {
+    snprintf(e, sizeof e, "output buffer length %zu != input length %zu", out_len, n);
+    return fail_quant(e);
+  }
+  float max_abs = 0.0f;
+  for (size_t i = 0; i < n; ++i) {
+    if (!isfinite(x[i])) {
+      rust_f32(f, sizeof f, x[i]);
+      snprintf(e, sizeof e, "non-finite activation value at index %zu: %s", i, f);
+      return fail_quant(e);
+    }
+    const float a = fabsf(x[i]);
+    if (a > max_abs) max_abs = a;
+  }
+  const float clamped = max_abs > 1e-5f ? max_abs : 1e-5f; /* f32::max(max_abs, 1e-5) */
+  *scale = clamped / 127.0f;
+  const float inv_scale = 127.0f / clamped;
+  for (size_t i = 0; i < n; ++i) {
+    float r = roundf(x[i] * inv_scale); /* f32::round: half away from zero */
+    if (r < -128.0f) r = -128.0f;
+    if (r > 127.0f) r = 127.0f;
+    out[i] = (int8_t)r;
+  }
+  return ok();
+}
+
+/* lib.rs:494-509, simd.rs:1135-1185 */
+int bnro_sqrelu_gate(const float *gate, size_t g_len, const float *up, size_t u_len,
+                     float *out, size_t out_len) {
+  char e[96], g[96];
+  if (g_len != u_len || g_len != out_len) {
+    snprintf(e, sizeof e, "gate.len() == up.len() == out.len() = %zu", g_len);
+    snprintf(g, sizeof g, "up.len()=%zu, out.len()=%zu", u_len, out_len);
+    return fail_shape(e, g);
+  }
+  for (size_t i = 0; i < g_len; ++i) {
+    const float r = gate[i] > 0.0f ? gate[i] : 0.0f; /* max_ps(g, 0): NaN -> 0 */
+    out[i] = r * r * up[i];
+  }
+  return ok();
+}

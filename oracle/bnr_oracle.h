@@ -140,6 +140,25 @@ int bnro_lm_head_matmul_i8(const float *hidden, size_t hidden_len, const int8_t 
                            float *output, size_t out_len, size_t vocab_size,
                            size_t hidden_size);
 
+/* ---- Layer glue ---- */
+
+/* simd::sum_squares_f32_fast  bitnet-cpu/src/simd.rs:802-839 (AVX2+FMA: 8 FMA
+ * lanes, hsum, unfused tail; scalar fallback: sequential sum of x*x). */
+float bnro_sum_squares_f32(const float *x, size_t n);
+/* norm::rms_norm  bitnet-cpu/src/norm.rs:76-136 (= CpuBackend::rms_norm,
+ * bitnet-cpu/src/lib.rs:268-270): rms = sqrt(sum_sq/d + eps), inv = 1/rms,
+ * out[i] = (x[i]*inv)*w[i] (mul_scale_f32_fast simd.rs:850-890). */
+int bnro_rms_norm(const float *input, size_t in_len, const float *weight, size_t w_len,
+                  float eps, float *output, size_t out_len);
+/* absmax::absmax_quantize_row_into  bitnet-core/src/quant/absmax.rs:127-170:
+ * scale = max(max|x|, 1e-5)/127, q = clamp(round(x*127/max), -128, 127). */
+int bnro_absmax_quantize_row(const float *x, size_t n, int8_t *out, size_t out_len,
+                             float *scale);
+/* CpuBackend::sqrelu_gate  bitnet-cpu/src/lib.rs:494-509 ->
+ * simd::sqrelu_gate_f32_fast simd.rs:1135-1185: out = (r*r)*up, r = max(gate, 0). */
+int bnro_sqrelu_gate(const float *gate, size_t g_len, const float *up, size_t u_len,
+                     float *out, size_t out_len);
+
 /* Number of OpenMP threads the attention head loop uses (Rayon sizes its
  * pool to all logical cores, lib.rs:99-133). 0 = all cores. */
 void bnro_set_threads(int n);
