@@ -387,6 +387,68 @@ def bench_lm_head(torch, be, steps: int = 20):
     return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
 
 
+def bench_model(torch, be, position: int = 1024, steps: int = 10):
+    """One decode token through the whole 2B stack on the device (30 layers:
+    norm/quantise, grouped ternary GEMVs, fused decode attention at context
+    `position`, residuals; final norm; i8 LM head), captured as one HIP graph
+    of 273 launches.  Synthetic weights (random packed bytes, every 2-bit
+    code), random cache rows 0..position-1."""
+    from bitnetrs_amd.model import DecodeModel, LayerWeights, ModelShape
+
+    s = ModelShape()
+    cap = 4096
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7080)
+    q_dim, kv_dim = s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim
+    shapes = [(q_dim, s.hidden), (kv_dim, s.hidden), (kv_dim, s.hidden), (s.hidden, q_dim),
+              (s.ffn, s.hidden), (s.ffn, s.hidden), (s.hidden, s.ffn)]
+
+    def packed(m, k):
+        return torch.randint(0, 256, (m * ((k + 3) // 4),), dtype=torch.uint8, device="cuda",
+                             generator=g)
+
+    def norm(n):
+        return 0.8 + 0.4 * torch.rand(n, device="cuda", generator=g)
+
+    layers = [LayerWeights(*[packed(m, k) for (m, k) in shapes], scales=(0.05,) * 7,
+                           attention_norm=norm(s.hidden), attn_sub_norm=norm(q_dim),
+                           ffn_norm=norm(s.hidden), ffn_sub_norm=norm(s.ffn))
+              for _ in range(s.n_layers)]
+    lm_w = torch.randint(-128, 128, (s.vocab * s.hidden,), dtype=torch.int8, device="cuda",
+                         generator=g)
+    dm = DecodeModel(be, s, layers, norm(s.hidden), lm_w,
+                     torch.rand(s.vocab, device="cuda", generator=g) * 0.01, cap)
+    for li in range(s.n_layers):
+        dm.cache.k[li][:, :position].normal_(generator=g)
+        dm.cache.v[li][:, :position].normal_(generator=g)
+    dm.cache.layer_lengths = [position] * s.n_layers
+    dm.cache.filled_positions = position
+    emb = torch.randn(s.hidden, device="cuda", generator=g)
+    h = emb.clone()
+    logits = torch.zeros(s.vocab, device="cuda")
+    dm.step(h, logits, position=position)  # eager warm-up (every launch once)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        h.copy_(emb)
+        dm.step(h, logits, position=position)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    nbytes = (s.n_layers * sum(gemv_bytes(m, k) for (m, k) in shapes)
+              + s.n_layers * decode_bytes(position + 1) + lm_head_bytes(s.vocab, s.hidden))
+    del layers, lm_w, dm
+    torch.cuda.empty_cache()
+    return {"ms": ms, "tok_s": 1e3 / ms, "bytes": nbytes, "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "position": position}
+
+
 def cpu_baseline_lm_head(budget_s: float):
     """The oracle's lm_head_matmul_i8 (AVX2+FMA rows over all host cores) at
     the 2B shape."""
@@ -524,6 +586,7 @@ def main() -> int:
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode")
     ap.add_argument("--no-gemv", action="store_true", help="skip the ternary GEMV workload")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the i8 LM head workload")
+    ap.add_argument("--no-model", action="store_true", help="skip the whole-model decode token")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -639,6 +702,16 @@ def main() -> int:
                          "traffic": traffic.get("lm_head_i8_kernel", {}).get("bytes_per_launch"),
                          "kernel": "lm_head_i8_kernel", "kernel_us": round(lm["us"], 3),
                          "bytes_per_launch": lm["bytes"]}}
+    if not args.no_model:
+        md = bench_model(torch, be)
+        log(f"model decode token (30 layers + LM head, context {md['position']}): "
+            f"{md['ms']:.3f} ms = {md['tok_s']:.0f} tok/s, {md['gbs']:.0f} GB/s")
+        line["model"] = {
+            "workload": "bitnet_2b_decode_token_30L_ctx1024_w2a8_i8head",
+            "value": round(md["tok_s"], 1), "unit": "tokens/s", "ms_per_token": round(md["ms"], 4),
+            "bytes_per_token": md["bytes"], "gbs": round(md["gbs"], 1),
+            "frac_hbm": round(md["gbs"] / HBM_PEAK_GBS, 4),
+            "timed": "one HIP graph per token: 30 x 9 launches + residual, final norm, LM head"}
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)

@@ -136,3 +136,71 @@ def batched_lengths(n: int = 32, lo: int = 128, hi: int = 4096, cfg: int = 4):
     seeded PCG64 stream."""
     rng = np.random.default_rng(seed(cfg, 15))
     return rng.integers(lo, hi, size=n).astype(np.int32)
+
+
+# ----------------------------------------------------------------------------
+# Whole decode token through the layer stack (oracle composition)
+# ----------------------------------------------------------------------------
+
+def make_decode_model(seed, hidden, n_heads, n_kv, head_dim, ffn, n_layers, vocab):
+    """Seeded synthetic BitNet weights: ternary projections (packed rows),
+    absmean scales, RMSNorm weights, i8 LM head with per-row scales."""
+    rng = np.random.default_rng(seed)
+    q_dim, kv_dim = n_heads * head_dim, n_kv * head_dim
+    shapes = [(q_dim, hidden), (kv_dim, hidden), (kv_dim, hidden), (hidden, q_dim),
+              (ffn, hidden), (ffn, hidden), (hidden, ffn)]
+    layers = []
+    for _ in range(n_layers):
+        mats = [oracle.pack_rows(rng.integers(-1, 2, size=s).astype(np.int8)) for s in shapes]
+        scales = [float(np.float32(rng.uniform(0.02, 0.08))) for _ in shapes]
+        norms = [rng.uniform(0.8, 1.2, size=n).astype(np.float32)
+                 for n in (hidden, q_dim, hidden, ffn)]
+        layers.append({"mats": mats, "shapes": shapes, "scales": scales, "norms": norms})
+    return {"layers": layers, "final_norm": rng.uniform(0.8, 1.2, hidden).astype(np.float32),
+            "lm_w": rng.integers(-128, 128, size=(vocab, hidden)).astype(np.int8),
+            "lm_scales": rng.uniform(0.001, 0.01, vocab).astype(np.float32),
+            "dims": (hidden, n_heads, n_kv, head_dim, ffn, n_layers, vocab)}
+
+
+def oracle_decode_token(model, h, position, cache, backend, theta=THETA, eps=1e-5):
+    """BitNetModel::forward_into's decode path for one token
+    (bitnet-model/src/lib.rs:946-1163) composed from the oracle's pinned
+    functions.  h [hidden] is updated in place; returns the logits."""
+    hidden, n_heads, n_kv, hd, ffn, n_layers, vocab = model["dims"]
+    f32 = np.float32
+
+    def gemv(mat, shape, scale, x_q, absmax):
+        out = np.zeros(shape[0], f32)
+        oracle.ternary_gemv_preq(mat, scale, x_q, absmax, out, shape[0], shape[1])
+        return out
+
+    def norm_quant(x, g):
+        y = np.zeros(x.size, f32)
+        oracle.rms_norm(x, g, eps, y)
+        q, sc = oracle.absmax_quantize_row(y)
+        return q, float(f32(f32(sc) * f32(127.0)))
+
+    for li, L in enumerate(model["layers"]):
+        m, sh, sc, nm = L["mats"], L["shapes"], L["scales"], L["norms"]
+        xq, aa = norm_quant(h, nm[0])
+        q, k, v = (gemv(m[i], sh[i], sc[i], xq, aa) for i in range(3))
+        backend.rope_embed(q, k, position, hd, n_heads, n_kv, theta)
+        cache.store_kv(li, position, k, v)
+        attn = np.zeros(n_heads * hd, f32)
+        backend.masked_attention(q, cache.k(li), cache.v(li), attn, n_heads, n_kv, hd, position)
+        xq, aa = norm_quant(attn, nm[1])
+        o = gemv(m[3], sh[3], sc[3], xq, aa)
+        oracle.axpy(1.0, o, h)
+        xq, aa = norm_quant(h, nm[2])
+        gate, up = gemv(m[4], sh[4], sc[4], xq, aa), gemv(m[5], sh[5], sc[5], xq, aa)
+        inner = np.zeros(ffn, f32)
+        oracle.sqrelu_gate(gate, up, inner)
+        xq, aa = norm_quant(inner, nm[3])
+        down = gemv(m[6], sh[6], sc[6], xq, aa)
+        oracle.axpy(1.0, down, h)
+    cache.advance()
+    fin = np.zeros(hidden, f32)
+    oracle.rms_norm(h, model["final_norm"], eps, fin)
+    logits = np.zeros(vocab, f32)
+    oracle.lm_head_matmul_i8(fin, model["lm_w"], model["lm_scales"], logits, vocab, hidden)
+    return logits

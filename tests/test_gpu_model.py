@@ -1,0 +1,70 @@
+"""A whole decode token through a small BitNet layer stack on the device
+(DecodeModel: norm/quantise, grouped ternary GEMVs, fused decode attention,
+residuals, final norm, i8 LM head) against the oracle's composition of the
+reference's decode path (bitnet-model/src/lib.rs:946-1163), over consecutive
+positions.
+
+The device sums RMSNorm squares in a tree (the reference: 8 AVX2 lanes), so
+a normalised value can differ in its last bit and, on a rounding half, its
+int8 quantisation by one; each such flip moves a projection output by about
+scale * act_absmax / 127.  Logits and the residual stream are therefore
+compared with a relative bound (1e-2 of their RMS at the worst element,
+1e-4 at the median) instead of the attention path's elementwise bound; the
+run reports the worst ratio it saw (about 1e-6 when no flip occurs)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from common import make_decode_model, oracle_decode_token
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[gpu case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("n_kv", [1, 2])
+def test_decode_model_matches_oracle(backend, n_kv):
+    case(f"decode model n_kv {n_kv}")
+    import torch
+
+    import bitnetrs_amd
+    from bitnetrs_amd.model import DecodeModel, LayerWeights, ModelShape
+
+    hidden, n_heads, hd, ffn, n_layers, vocab, cap = 512, 4, 128, 1024, 2, 1000, 16
+    model = make_decode_model(77 + n_kv, hidden, n_heads, n_kv, hd, ffn, n_layers, vocab)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    layers = []
+    for L in model["layers"]:
+        m = [d(x.reshape(-1)) for x in L["mats"]]
+        layers.append(LayerWeights(*m, scales=tuple(L["scales"]), attention_norm=d(L["norms"][0]),
+                                   attn_sub_norm=d(L["norms"][1]), ffn_norm=d(L["norms"][2]),
+                                   ffn_sub_norm=d(L["norms"][3])))
+    shape = ModelShape(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=ffn,
+                       n_layers=n_layers, vocab=vocab)
+    dm = DecodeModel(backend, shape, layers, d(model["final_norm"]), d(model["lm_w"].reshape(-1)),
+                     d(model["lm_scales"]), cap)
+    cache = oracle.KVCache(n_layers, n_kv, hd, cap)
+    be = oracle.CpuBackend()
+    rng = np.random.default_rng(5)
+    worst = 0.0
+    for pos in range(6):
+        emb = rng.standard_normal(hidden).astype(np.float32)
+        h_ref = emb.copy()
+        logits_ref = oracle_decode_token(model, h_ref, pos, cache, be)
+        h = d(emb)
+        logits = torch.zeros(vocab, device="cuda")
+        dm.step(h, logits)
+        torch.cuda.synchronize()
+        for got, ref in ((logits.cpu().numpy(), logits_ref), (h.cpu().numpy(), h_ref)):
+            err = np.abs(got.astype(np.float64) - ref)
+            rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+            worst = max(worst, err.max() / rms)
+            assert err.max() <= 1e-2 * rms, (pos, err.max(), rms)
+            assert np.median(err) <= 1e-4 * rms, (pos, np.median(err), rms)
+    assert dm.position == 6 and len(cache) == 6
+    print(f"worst max|err| / rms: {worst:.2e}")
