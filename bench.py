@@ -387,7 +387,7 @@ def bench_lm_head(torch, be, steps: int = 20):
     return {"us": us, "bytes": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
 
 
-def bench_model(torch, be, position: int = 1024, steps: int = 10):
+def bench_model(torch, be, position: int = 1024, steps: int = 10, fused: bool = False):
     """One decode token through the whole 2B stack on the device (30 layers:
     norm/quantise, grouped ternary GEMVs, fused decode attention at context
     `position`, residuals; final norm; i8 LM head), captured as one HIP graph
@@ -416,7 +416,7 @@ def bench_model(torch, be, position: int = 1024, steps: int = 10):
     lm_w = torch.randint(-128, 128, (s.vocab * s.hidden,), dtype=torch.int8, device="cuda",
                          generator=g)
     dm = DecodeModel(be, s, layers, norm(s.hidden), lm_w,
-                     torch.rand(s.vocab, device="cuda", generator=g) * 0.01, cap)
+                     torch.rand(s.vocab, device="cuda", generator=g) * 0.01, cap, fused=fused)
     for li in range(s.n_layers):
         dm.cache.k[li][:, :position].normal_(generator=g)
         dm.cache.v[li][:, :position].normal_(generator=g)
@@ -704,6 +704,8 @@ def main() -> int:
                          "bytes_per_launch": lm["bytes"]}}
     if not args.no_model:
         md = bench_model(torch, be)
+        mf = bench_model(torch, be, fused=True)
+        log(f"model decode token, glue folded into the projections: {mf['ms']:.3f} ms")
         log(f"model decode token (30 layers + LM head, context {md['position']}): "
             f"{md['ms']:.3f} ms = {md['tok_s']:.0f} tok/s, {md['gbs']:.0f} GB/s")
         line["model"] = {
@@ -711,6 +713,7 @@ def main() -> int:
             "value": round(md["tok_s"], 1), "unit": "tokens/s", "ms_per_token": round(md["ms"], 4),
             "bytes_per_token": md["bytes"], "gbs": round(md["gbs"], 1),
             "frac_hbm": round(md["gbs"] / HBM_PEAK_GBS, 4),
+            "ms_per_token_glue_in_gemv": round(mf["ms"], 4),
             "timed": "one HIP graph per token: 30 x 9 launches + residual, final norm, LM head"}
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")

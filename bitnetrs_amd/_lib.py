@@ -123,6 +123,9 @@ SIGNATURES = {
     "bnr_dev_absmax_quantize": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp]),
     "bnr_dev_norm_quant": (_c.c_int, [_vp, _c.c_int, _vp, _vp, _vp, _c.c_float, _sz, _vp, _vp,
                                       _vp, _vp]),
+    "bnr_dev_ternary_gemv_norm_group": (_c.c_int, [_vp, _sz, _c.POINTER(_vp), _f, _c.c_int, _vp,
+                                                   _vp, _vp, _c.c_float, _vp, _c.POINTER(_vp),
+                                                   _c.POINTER(_sz), _sz, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
 }
 

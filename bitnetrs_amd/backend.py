@@ -243,6 +243,21 @@ class HipBackend:
             self._h, n, wp, sc, _dev(activation_q, "activation_q", dtype=torch.int8),
             _dev(act_absmax, "act_absmax"), op, mf, in_features, _stream(stream)))
 
+    def dev_ternary_gemv_norm_group(self, weights, weight_scales, mode, a, b, gamma, eps, h_out,
+                                    outputs, out_features, in_features, stream=None) -> None:
+        """Grouped ternary GEMV whose prologue forms x (mode), RMSNorms and
+        quantises it: the glue launch folded into the projection."""
+        import torch
+
+        n = len(weights)
+        wp = (ctypes.c_void_p * n)(*[_dev(w, "weight", dtype=torch.uint8).value for w in weights])
+        op = (ctypes.c_void_p * n)(*[_dev(o, "output").value for o in outputs])
+        sc = (ctypes.c_float * n)(*[float(x) for x in weight_scales])
+        mf = (ctypes.c_size_t * n)(*[int(x) for x in out_features])
+        _lib.check(self._L.bnr_dev_ternary_gemv_norm_group(
+            self._h, n, wp, sc, int(mode), _dev(a, "a"), _dev(b, "b", True), _dev(gamma, "gamma"),
+            eps, _dev(h_out, "h_out", True), op, mf, in_features, _stream(stream)))
+
     def dev_rms_norm(self, input, weight, eps, output, n, stream=None) -> None:
         _lib.check(self._L.bnr_dev_rms_norm(self._h, _dev(input, "input"), _dev(weight, "weight"),
                                             eps, _dev(output, "output"), n, _stream(stream)))

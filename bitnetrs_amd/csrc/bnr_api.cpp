@@ -1421,6 +1421,61 @@ extern "C" int bnr_dev_ternary_gemv_preq_group_devscale(
                         outputs, out_features, in_features, (hipStream_t)stream);
 }
 
+extern "C" int bnr_dev_ternary_gemv_norm_group(
+    bnr_ctx *c, size_t n, const uint8_t *const *weight_packed, const float *weight_scales,
+    int mode, const float *a, const float *b, const float *gamma, float eps, float *h_out,
+    float *const *outputs, const size_t *out_features, size_t in_features, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (n == 0 || n > (size_t)kMaxGemvGroup)
+    return err_config(fmt("ternary GEMV group size must be 1..%d, got %zu", kMaxGemvGroup, n));
+  if (mode != BNR_GLUE_PLAIN && mode != BNR_GLUE_RESIDUAL && mode != BNR_GLUE_SQRELU)
+    return err_config(fmt("unknown norm_quant mode %d", mode));
+  if (eps <= 0.0f || !std::isfinite(eps))
+    return err_quant("eps must be finite and > 0, got " + rust_f32(eps));
+  if (in_features == 0) return err_quant("cannot quantise an empty activation vector");
+  if (in_features > (size_t)kMaxNormGemvK)
+    return err_backend(fmt("ternary_gemv_norm_group: in_features %zu > %d is not supported "
+                           "(use bnr_dev_norm_quant + bnr_dev_ternary_gemv_preq_group_devscale)",
+                           in_features, kMaxNormGemvK));
+  if (!weight_packed || !weight_scales || !outputs || !out_features || !a || !gamma ||
+      (mode != BNR_GLUE_PLAIN && !b) || (mode == BNR_GLUE_RESIDUAL && !h_out))
+    return err_backend("ternary_gemv_norm_group: NULL pointer");
+  if (h_out && (h_out == a || h_out == b))
+    return err_backend("ternary_gemv_norm_group: h_out must not alias a or b");
+  TernaryGemvGroupArgs g{};
+  g.n = (int)n;
+  g.in_features = (int)in_features;
+  g.packed_cols = (long long)((in_features + 3) / 4);
+  bool vec = g.packed_cols % 16 == 0;
+  int wgs = 0;
+  for (size_t i = 0; i < n; ++i) {
+    int st = check_gemv(SIZE_MAX, weight_scales[i], SIZE_MAX, 1.0f, SIZE_MAX, out_features[i],
+                        in_features);
+    if (st) return st;
+    if (out_features[i] && (!weight_packed[i] || !outputs[i]))
+      return err_backend("ternary_gemv_norm_group: NULL pointer");
+    g.weight[i] = weight_packed[i];
+    g.out[i] = outputs[i];
+    g.weight_scale[i] = weight_scales[i];
+    g.out_features[i] = (int)out_features[i];
+    g.wg_off[i] = wgs;
+    wgs += (int)((out_features[i] + 15) / 16);
+    vec = vec && ((uintptr_t)weight_packed[i] % 16) == 0;
+  }
+  for (size_t i = n; i <= (size_t)kMaxGemvGroup; ++i) g.wg_off[i] = wgs;
+  if (wgs == 0) return set_ok();
+  GemvNormArgs p{};
+  p.mode = mode;
+  p.a = a;
+  p.b = b;
+  p.gamma = gamma;
+  p.eps = eps;
+  p.h_out = mode == BNR_GLUE_RESIDUAL ? h_out : nullptr;
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_ternary_gemv_norm(g, p, vec, (hipStream_t)stream), "ternary_gemv_norm launch");
+  return set_ok();
+}
+
 // ---------------------------------------------------------------------------
 // Layer glue
 // ---------------------------------------------------------------------------

@@ -169,7 +169,162 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
   gemv_rows<VEC>(w, a.act, out, m, a.in_features, a.packed_cols, scale, b - off, s_act);
 }
 
+// ---------------------------------------------------------------------------
+// Ternary GEMV with the activation's RMSNorm and int8 quantisation as its
+// prologue (the glue launch folded into the projection).  Every workgroup
+// forms x from f32 inputs (a | a + b | max(a,0)^2 * b), reduces sum(x^2) and
+// max|y| with the same tree, and so derives the same int8 activations and
+// the same scale as norm_quant_kernel would; the int8 vector never leaves
+// LDS.  The workgroup issues its weight loads first, so the prologue runs
+// under their latency.  K <= 8192 (one LDS pass); workgroup 0 writes h_out
+// (mode residual), which must not alias a or b.
+// ---------------------------------------------------------------------------
+constexpr int kNormK = 8192;
+constexpr int kNormGroups = kNormK / 16;     // 16-activation groups
+constexpr int kNormPieces = kNormK / 64;     // 16-byte weight pieces per row
+constexpr int kNormPiecesPerLane = kNormPieces / 16;
+constexpr int kNormGroupsPerThread = kNormGroups / 256;
+
+__device__ __forceinline__ float norm_x(const GemvNormArgs &p, int i) {
+#pragma clang fp contract(off)
+  const float u = p.a[i];
+  if (p.mode == kGlueResidual) return u + p.b[i];
+  if (p.mode == kGlueSqrelu) {
+    const float r = fmaxf(u, 0.0f);
+    return r * r * p.b[i];
+  }
+  return u;
+}
+
+__device__ __forceinline__ float norm_y(float x, float inv, float g) {
+#pragma clang fp contract(off)
+  return x * inv * g;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroupArgs a,
+                                                                GemvNormArgs p) {
+  __shared__ uint4 s_act[kNormGroups];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15, lane = tid & 63, wv_id = tid >> 6;
+  const int b = blockIdx.x;
+  const uint8_t *w = a.weight[0];
+  float *out = a.out[0];
+  float ws = a.weight_scale[0];
+  int m = a.out_features[0], off = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGemvGroup; ++i) {
+    if (i < a.n && b >= a.wg_off[i]) {
+      w = a.weight[i];
+      out = a.out[i];
+      ws = a.weight_scale[i];
+      m = a.out_features[i];
+      off = a.wg_off[i];
+    }
+  }
+  const int K = a.in_features, nb = (K + 3) / 4;
+  const int row = (b - off) * kRowsPerWg + slot;
+  const long long b0 = (long long)min(row, m - 1) * a.packed_cols;
+  // 1. this lane's weight pieces (in flight during the prologue)
+  uint4 wq[kNormPiecesPerLane];
+#pragma unroll
+  for (int i = 0; i < kNormPiecesPerLane; ++i) {
+    const int c = j + 16 * i;
+    if (VEC)
+      wq[i] = 16 * c < nb ? *reinterpret_cast<const uint4 *>(w + b0 + 16 * c) : make_uint4(0, 0, 0, 0);
+    else
+      wq[i] = 16 * c < nb ? load16_bounded(w, b0 + 16 * c, b0 + nb) : make_uint4(0, 0, 0, 0);
+  }
+  // 2. x for groups tid, tid+256 (16 consecutive elements each), sum of squares
+  float x[kNormGroupsPerThread][16], g[kNormGroupsPerThread][16];
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < kNormGroupsPerThread; ++q) {
+    const int e0 = 16 * (tid + 256 * q);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int i = e0 + e;
+      x[q][e] = i < K ? norm_x(p, i) : 0.f;
+      g[q][e] = i < K ? p.gamma[i] : 0.f;
+      ss = fmaf(x[q][e], x[q][e], ss);
+    }
+  }
+  if (p.h_out && b == 0) {
+#pragma unroll
+    for (int q = 0; q < kNormGroupsPerThread; ++q)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (16 * (tid + 256 * q) + e < K) p.h_out[16 * (tid + 256 * q) + e] = x[q][e];
+  }
+  // block sum (4 waves); the same tree in every workgroup
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if (lane == 0) red[wv_id] = ss;
+  __syncthreads();
+  const float sum_sq = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = 1.0f / sqrtf(sum_sq / (float)K + p.eps);
+  float mx = 0.f;
+#pragma unroll
+  for (int q = 0; q < kNormGroupsPerThread; ++q)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      x[q][e] = norm_y(x[q][e], inv, g[q][e]);  // zero past K (x = 0)
+      mx = fmaxf(mx, fabsf(x[q][e]));
+    }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  __syncthreads();  // everyone has read red[] as sums
+  if (lane == 0) red[wv_id] = mx;
+  __syncthreads();
+  const float mm = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), 1e-5f);
+  const float scale = mm / 127.0f, inv_scale = 127.0f / mm;
+  // 3. int8 activations into LDS, transposed as the GEMV reads them
+#pragma unroll
+  for (int q = 0; q < kNormGroupsPerThread; ++q) {
+    unsigned d[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      d[t] = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int qv = (int)fminf(fmaxf(roundf(x[q][4 * t + e] * inv_scale), -128.0f), 127.0f);
+        d[t] |= (unsigned)(qv & 0xFF) << (8 * e);
+      }
+    }
+    const int gi = tid + 256 * q;
+    s_act[(gi & 3) * kNormPieces + (gi >> 2)] = transpose_bytes(make_uint4(d[0], d[1], d[2], d[3]));
+  }
+  __syncthreads();
+  // 4. the projection
+  int acc = 0;
+#pragma unroll
+  for (int i = 0; i < kNormPiecesPerLane; ++i) {
+    const int c = j + 16 * i;
+    if (16 * c < nb) {
+      acc = dot16(wq[i].x, s_act[c], acc);
+      acc = dot16(wq[i].y, s_act[kNormPieces + c], acc);
+      acc = dot16(wq[i].z, s_act[2 * kNormPieces + c], acc);
+      acc = dot16(wq[i].w, s_act[3 * kNormPieces + c], acc);
+    }
+  }
+  acc = row_sum16_i(acc);
+  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), act_scale = scale * 127
+  const float t = ws * (scale * 127.0f);
+  const float cs = t / 127.0f;
+  if (j == 0 && row < m) out[row] = (float)acc * cs;
+}
+
 }  // namespace
+
+hipError_t launch_ternary_gemv_norm(const TernaryGemvGroupArgs &a, const GemvNormArgs &p, bool vec,
+                                    hipStream_t s) {
+  const int wgs = a.wg_off[a.n];
+  if (wgs <= 0) return hipSuccess;
+  if (a.in_features > kNormK) return hipErrorInvalidValue;
+  if (vec)
+    ternary_gemv_norm_kernel<true><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  else
+    ternary_gemv_norm_kernel<false><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  return hipGetLastError();
+}
 
 hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s) {
   const int wgs = a.wg_off[a.n];

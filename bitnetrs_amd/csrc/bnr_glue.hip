@@ -81,9 +81,13 @@ __global__ __launch_bounds__(kNormLanes) void norm_quant_kernel(NormQuantArgs a)
   __shared__ float red[kNormLanes / 64];
   const int tid = threadIdx.x;
   const bool cached = a.n <= kNormLanes * kNormCache;
-  float v[kNormCache];
-  // phase 1: x (and h_out), sum of squares
+  float v[kNormCache], gm[kNormCache];
   float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormCache; ++k) {
+    const int i = tid + kNormLanes * k;
+    gm[k] = a.gamma && i < a.n ? a.gamma[i] : 1.0f;
+  }
 #pragma unroll
   for (int k = 0; k < kNormCache; ++k) {
     const int i = tid + kNormLanes * k;
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(kNormLanes) void norm_quant_kernel(NormQuantArgs a)
   for (int k = 0; k < kNormCache; ++k) {
     const int i = tid + kNormLanes * k;
     if (i < a.n) {
-      if (a.gamma) v[k] = glue_y(v[k], inv, a.gamma[i]);
+      if (a.gamma) v[k] = glue_y(v[k], inv, gm[k]);
       if (a.y_out) a.y_out[i] = v[k];
       mx = fmaxf(mx, fabsf(v[k]));
     }

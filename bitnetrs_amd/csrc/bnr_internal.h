@@ -134,6 +134,23 @@ struct TernaryGemvGroupArgs {
 };
 hipError_t launch_ternary_gemv_group(const TernaryGemvGroupArgs &a, bool vec, hipStream_t s);
 
+// Modes of the layer-glue input x.
+constexpr int kGluePlain = 0;     // x = a
+constexpr int kGlueResidual = 1;  // x = a + b, written to h_out
+constexpr int kGlueSqrelu = 2;    // x = max(a, 0)^2 * b
+
+// Prologue of the norm-fused GEMV: x from a (and b) per mode (kGlue*),
+// y = RMSNorm(x) with gamma, int8 absmax quantisation of y in LDS.
+struct GemvNormArgs {
+  int mode;
+  const float *a, *b, *gamma;
+  float eps;
+  float *h_out;  // mode residual: a + b, written by workgroup 0; must not alias a or b
+};
+constexpr int kMaxNormGemvK = 8192;
+hipError_t launch_ternary_gemv_norm(const TernaryGemvGroupArgs &a, const GemvNormArgs &p, bool vec,
+                                    hipStream_t s);
+
 // LM head with i8 weights: out[v] = dot(weight[v], hidden) * scales[v].
 struct LmHeadArgs {
   const float *hidden;
@@ -147,9 +164,6 @@ struct LmHeadArgs {
 hipError_t launch_lm_head_i8(const LmHeadArgs &a, bool vec, hipStream_t s);
 
 // Layer glue (bnr_glue.hip).
-constexpr int kGluePlain = 0;     // x = a
-constexpr int kGlueResidual = 1;  // x = a + b, written to h_out
-constexpr int kGlueSqrelu = 2;    // x = max(a, 0)^2 * b
 struct NormQuantArgs {
   int mode;
   const float *a, *b;

@@ -6,18 +6,20 @@ RoPE + KV append + attention, attention sub-norm + quantisation, the o
 projection, residual, FFN norm + quantisation, gate/up, squared-ReLU gate +
 sub-norm + quantisation, the down projection and the residual; then the
 final norm and the i8 LM head.  ``DecodeModel`` keeps weights, KV caches and
-activations in HBM and issues, per layer, nine launches of this library:
+activations in HBM.  With ``fused=True`` (the default) a layer is five
+launches of this library, each projection computing the RMSNorm and int8
+quantisation of its input as its own prologue:
 
-  norm_quant (attention norm; for layers after the first it also adds the
-  previous layer's FFN output to the residual stream) -> q/k/v GEMV (one
-  grouped launch) -> fused decode step -> norm_quant (attention sub-norm) ->
-  o GEMV -> norm_quant (residual + FFN norm) -> gate/up GEMV (grouped) ->
-  norm_quant (sqrelu gate + FFN sub-norm) -> down GEMV
+  q/k/v GEMV (attention norm; after the first layer it also adds the
+  previous layer's FFN output to the residual stream) -> fused decode step
+  -> o GEMV (attention sub-norm) -> gate/up GEMV (residual + FFN norm) ->
+  down GEMV (sqrelu gate + FFN sub-norm)
 
-and after the last layer a residual add, the final RMSNorm and the LM head.
-The activation scale travels between the norm/quantise launch and the GEMV
-in device memory, so a token needs no host round trip and can be captured
-in one HIP graph.  Weights are the caller's packed device tensors.
+With ``fused=False`` each glue step is its own launch (``bnr_dev_norm_quant``)
+and the projection reads the int8 vector and its scale from device memory:
+nine launches per layer.  After the last layer: residual, final RMSNorm,
+LM head.  A token needs no host round trip and can be captured in one HIP
+graph.  Weights are the caller's packed device tensors.
 """
 from __future__ import annotations
 
@@ -60,10 +62,10 @@ class ModelShape:
 
 class DecodeModel:
     def __init__(self, backend: HipBackend, shape: ModelShape, layers, final_norm, lm_head_i8,
-                 lm_head_scales, max_seq: int):
+                 lm_head_scales, max_seq: int, fused: bool = True):
         import torch
 
-        self.be, self.s = backend, shape
+        self.be, self.s, self.fused = backend, shape, fused
         self.layers = list(layers)
         assert len(self.layers) == shape.n_layers
         self.final_norm, self.lm_w, self.lm_scales = final_norm, lm_head_i8, lm_head_scales
@@ -78,6 +80,7 @@ class DecodeModel:
         self.final_normed = dev(s.hidden)
         self.q8 = torch.zeros(max(s.hidden, s.ffn, self.q_dim), dtype=torch.int8, device="cuda")
         self.act_absmax = dev(1)
+        self.hbuf = [dev(s.hidden), dev(s.hidden)]  # residual stream, double-buffered
 
     @property
     def position(self) -> int:
@@ -86,8 +89,56 @@ class DecodeModel:
     def step(self, h, logits, position: int = None, stream=None) -> None:
         """One token: h [hidden] (the embedding; updated in place to the
         residual stream after the last layer), logits [vocab]."""
-        be, s = self.be, self.s
         pos = self.position if position is None else position
+        if self.fused:
+            self._step_fused(h, logits, pos, stream)
+        else:
+            self._step_glue(h, logits, pos, stream)
+        if position is None:
+            self.cache.advance(1)
+
+    def _step_fused(self, h, logits, pos, stream) -> None:
+        be, s = self.be, self.s
+        cur, nxt = h, self.hbuf[0]
+        for li, w in enumerate(self.layers):
+            self.cache.check_store(li, pos, 1)
+            if li == 0:
+                be.dev_ternary_gemv_norm_group(
+                    [w.q, w.k, w.v], w.scales[0:3], BNR_GLUE_PLAIN, cur, None, w.attention_norm,
+                    s.eps, None, [self.qb, self.kb, self.vb],
+                    [self.q_dim, self.kv_dim, self.kv_dim], s.hidden, stream=stream)
+            else:  # previous layer's FFN output joins the residual stream first
+                be.dev_ternary_gemv_norm_group(
+                    [w.q, w.k, w.v], w.scales[0:3], BNR_GLUE_RESIDUAL, cur, self.ffn_out,
+                    w.attention_norm, s.eps, nxt, [self.qb, self.kb, self.vb],
+                    [self.q_dim, self.kv_dim, self.kv_dim], s.hidden, stream=stream)
+                cur, nxt = nxt, self._other(nxt)
+            be.dev_decode_step(self.qb, self.kb, self.vb, pos, s.n_heads, s.n_kv_heads,
+                               s.head_dim, s.theta, self.cache.k[li], self.cache.v[li],
+                               self.cache.max_seq, self.attn, stream=stream)
+            self.cache.mark_stored(li, pos, 1)
+            be.dev_ternary_gemv_norm_group(
+                [w.o], w.scales[3:4], BNR_GLUE_PLAIN, self.attn, None, w.attn_sub_norm, s.eps,
+                None, [self.o_out], [s.hidden], self.q_dim, stream=stream)
+            be.dev_ternary_gemv_norm_group(
+                [w.gate, w.up], w.scales[4:6], BNR_GLUE_RESIDUAL, cur, self.o_out, w.ffn_norm,
+                s.eps, nxt, [self.gate, self.up], [s.ffn, s.ffn], s.hidden, stream=stream)
+            cur, nxt = nxt, self._other(nxt)
+            be.dev_ternary_gemv_norm_group(
+                [w.down], w.scales[6:7], BNR_GLUE_SQRELU, self.gate, self.up, w.ffn_sub_norm,
+                s.eps, None, [self.ffn_out], [s.hidden], s.ffn, stream=stream)
+        if cur is not h:
+            h.copy_(cur)
+        be.dev_residual_add(h, self.ffn_out, s.hidden, stream=stream)
+        be.dev_rms_norm(h, self.final_norm, s.eps, self.final_normed, s.hidden, stream=stream)
+        be.dev_lm_head_matmul_i8(self.final_normed, self.lm_w, self.lm_scales, logits, s.vocab,
+                                 s.hidden, stream=stream)
+
+    def _other(self, buf):
+        return self.hbuf[1] if buf is self.hbuf[0] else self.hbuf[0]
+
+    def _step_glue(self, h, logits, pos, stream) -> None:
+        be, s = self.be, self.s
         for li, w in enumerate(self.layers):
             self.cache.check_store(li, pos, 1)
             if li == 0:
@@ -123,5 +174,3 @@ class DecodeModel:
         be.dev_rms_norm(h, self.final_norm, s.eps, self.final_normed, s.hidden, stream=stream)
         be.dev_lm_head_matmul_i8(self.final_normed, self.lm_w, self.lm_scales, logits, s.vocab,
                                  s.hidden, stream=stream)
-        if position is None:
-            self.cache.advance(1)

@@ -279,6 +279,20 @@ int bnr_dev_norm_quant(bnr_ctx *ctx, int mode, const float *a, const float *b, c
                        float eps, size_t n, float *h_out, int8_t *q_out, float *act_absmax,
                        void *stream);
 
+/* The glue launch folded into the projection: bnr_dev_norm_quant's x (mode,
+ * a, b), RMSNorm with gamma and int8 quantisation computed by every
+ * workgroup of the grouped ternary GEMV as its prologue, the int8
+ * activations kept in LDS.  One launch instead of two between the layer's
+ * norms and projections.  in_features <= 8192; mode BNR_GLUE_RESIDUAL
+ * writes a + b to h_out, which must not alias a or b (double-buffer the
+ * residual stream).  Outputs agree with norm_quant followed by the
+ * devscale GEMV to the rounding of the sum of squares. */
+int bnr_dev_ternary_gemv_norm_group(bnr_ctx *ctx, size_t n, const uint8_t *const *weight_packed,
+                                    const float *weight_scales, int mode, const float *a,
+                                    const float *b, const float *gamma, float eps, float *h_out,
+                                    float *const *outputs, const size_t *out_features,
+                                    size_t in_features, void *stream);
+
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
 

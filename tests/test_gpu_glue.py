@@ -119,11 +119,14 @@ def test_absmax_quantize_bit_exact(backend, n):
     assert float(host(s)[0]) == s_ref
 
 
-@pytest.mark.parametrize("mode,n", [(0, 2560), (1, 2560), (2, 6912), (0, 10001), (1, 9000)])
-def test_norm_quant_fused(backend, mode, n):
+@pytest.mark.parametrize("mode,n,alias", [(0, 2560, False), (1, 2560, False), (2, 6912, False),
+                                          (0, 10001, False), (1, 9000, False), (1, 9000, True),
+                                          (1, 2561, True), (2, 37, False)])
+def test_norm_quant_fused(backend, mode, n, alias):
     """The fused launch equals rms_norm followed by absmax_quantize on the GPU
-    (bit for bit), and the oracle's composition to rounding."""
-    case(f"norm_quant mode {mode} n {n}")
+    (bit for bit), and the oracle's composition to rounding.  alias: the
+    residual stream is updated in place (h_out is a)."""
+    case(f"norm_quant mode {mode} n {n} alias {alias}")
     import torch
 
     import bitnetrs_amd
@@ -145,7 +148,7 @@ def test_norm_quant_fused(backend, mode, n):
     q_ref, s_ref = oracle.absmax_quantize_row(y_ref)
 
     da, db, dg = dev(a), dev(b), dev(g)
-    h_out = torch.full((n,), float("nan"), device="cuda")
+    h_out = da if alias else torch.full((n,), float("nan"), device="cuda")
     q = torch.zeros(n, dtype=torch.int8, device="cuda")
     aa = torch.zeros(1, device="cuda")
     backend.dev_norm_quant(mode, da, db, dg, 1e-5, n, h_out, q, aa)

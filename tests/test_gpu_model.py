@@ -27,9 +27,9 @@ def case(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("n_kv", [1, 2])
-def test_decode_model_matches_oracle(backend, n_kv):
-    case(f"decode model n_kv {n_kv}")
+@pytest.mark.parametrize("n_kv,fused", [(1, True), (2, True), (1, False)])
+def test_decode_model_matches_oracle(backend, n_kv, fused):
+    case(f"decode model n_kv {n_kv} fused {fused}")
     import torch
 
     import bitnetrs_amd
@@ -47,7 +47,7 @@ def test_decode_model_matches_oracle(backend, n_kv):
     shape = ModelShape(hidden=hidden, n_heads=n_heads, n_kv_heads=n_kv, head_dim=hd, ffn=ffn,
                        n_layers=n_layers, vocab=vocab)
     dm = DecodeModel(backend, shape, layers, d(model["final_norm"]), d(model["lm_w"].reshape(-1)),
-                     d(model["lm_scales"]), cap)
+                     d(model["lm_scales"]), cap, fused=fused)
     cache = oracle.KVCache(n_layers, n_kv, hd, cap)
     be = oracle.CpuBackend()
     rng = np.random.default_rng(5)
