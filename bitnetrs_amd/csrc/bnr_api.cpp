@@ -183,6 +183,8 @@ struct bnr_ctx {
   size_t pf_ws_floats = 0;
   unsigned *pf_counters = nullptr;
   size_t n_pf_counters = 0;
+  unsigned *pf_queue = nullptr;  // persistent prefill: next item, workgroups done
+  size_t n_pf_queue = 0;
 
   // host-path staging
   float *d_q = nullptr, *d_k = nullptr, *d_out = nullptr;
@@ -204,6 +206,7 @@ struct bnr_ctx {
   // prefill planner
   int n_cu = 256;
   int pf_chunk_shift = -1;  // -1: planner decides; else key tiles per chunk = 2^shift
+  int pf_persistent = 0;    // 1: resident workgroups take prefill items from a queue
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> chunk shift) plans
 };
 
@@ -615,6 +618,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   }
   if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
   if (const char *v = std::getenv("BNR_PREFILL_CHUNK_SHIFT")) c->pf_chunk_shift = std::min(std::max(atoi(v), 0), 20);
+  if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT")) c->pf_persistent = atoi(v) > 0;
   *out = c;
   return set_ok();
 }
@@ -635,6 +639,7 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     if (c->ws_ml) (void)hipFree(c->ws_ml);
     if (c->counters) (void)hipFree(c->counters);
     if (c->pf_counters) (void)hipFree(c->pf_counters);
+    if (c->pf_queue) (void)hipFree(c->pf_queue);
     if (c->stream) (void)hipStreamDestroy(c->stream);
   }
   delete c;
@@ -1207,7 +1212,15 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
       pa.ws = c->pf_ws;
       pa.counters = c->pf_counters;
     }
-    HIP_TRY(launch_prefill(pa, group, s), "prefill launch");
+    int pwgs = 0;
+    if (c->pf_persistent > 0) {
+      st = ensure_zeroed(&c->pf_queue, &c->n_pf_queue, 2 * kCounterStride);
+      if (st) return st;
+      pa.queue = c->pf_queue;
+      const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
+      pwgs = (int)std::min<long long>((long long)n_kv_heads * plan.n_items, (long long)c->n_cu * per_cu);
+    }
+    HIP_TRY(launch_prefill(pa, group, pwgs, s), "prefill launch");
     return set_ok();
   }
   if (fast_shape(n_heads, n_kv_heads, head_dim) && aligned16(q) && aligned16(k_cache) &&

@@ -90,6 +90,7 @@ struct PrefillArgs {
   int n_items;                       // (query tile, chunk) items per kv head
   float *ws;                         // partial states: [n_kv][n_items][G][66][64]
   unsigned *counters;                // [n_kv][n_qtiles] x kCounterStride, zero between launches
+  unsigned *queue;                   // persistent launch: next item, workgroups done (2 x kCounterStride), zero between launches
 };
 // (query tile, chunk) items per kv head of a prefill launch, and the key
 // tiles they cover in total.
@@ -99,7 +100,8 @@ struct PrefillPlan {
   bool split;  // some query tile has more than one chunk
 };
 PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift);
-hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s);
+// persistent_wgs > 0: that many resident workgroups take items from a.queue.
+hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, hipStream_t s);
 bool prefill_supported(int group);
 
 // W2A8 ternary GEMV: out[i] = (float)dot(W[i], act) * scale, W packed 2 bits

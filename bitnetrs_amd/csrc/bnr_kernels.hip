@@ -162,20 +162,21 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 }
 
 // Merge the nsplit partial states of (sequence b, kv head h) into the
-// output.  CH splits per round: one load round trip, then wave w computes
-// the round's max and split weights of q head g = w, w+4, ... (one lane per
-// split, wave reductions), and every lane forms its outputs as an
-// independent weighted sum.  AGENT: the partials were written by other
-// workgroups of this launch (agent-coherent loads); otherwise by an earlier
-// kernel (plain loads).  lds: at least 64*G + 3*G floats.
-template <int G, bool AGENT>
+// output.  CH (<= 64) splits per round: one load round trip, then wave w
+// computes the round's max and split weights of q head g = w, w+4, ... (one
+// lane per split, wave reductions), and every lane forms its outputs as an
+// independent weighted sum.  CH is matched to the split count so that no
+// load is spent on a clamped duplicate.  AGENT: the partials were written by
+// other workgroups of this launch (agent-coherent loads); otherwise by an
+// earlier kernel (plain loads).  lds: at least 64*G + 3*G floats.
+template <int G, bool AGENT, int CH>
 __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, int nsplit,
                                              float *lds) {
+  static_assert(CH % 4 == 0 && CH <= 64, "splits per round: one per lane of a wave");
   constexpr int D = kHeadDim;
   constexpr int NE = G * D;                 // output elements of this kv head
   constexpr int EPL = NE >= 512 ? 2 : 1;    // adjacent elements per lane (one 8-byte load)
   constexpr int NT = NE / EPL;              // lanes with work (<= 256)
-  constexpr int CH = 64;                    // splits per round (one per lane of a wave)
   constexpr int GPW = (G + 3) / 4;          // q heads per wave
   float *s_w = lds;             // [G][CH] split weights of the round
   float *s_M = s_w + CH * G;    // [G] running max
@@ -199,8 +200,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
     // One batch of loads; split indices past the end are clamped (their
     // weight is zero), so there are no branches between loads.
     float ov[EPL][CH];
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
+    auto load_o = [&](int u) {
       const float *pu = po + (long long)min(c0 + u, nsplit - 1) * step + e0;
       if (EPL == 2) {
         const unsigned long long r =
@@ -213,15 +213,18 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
       } else {
         ov[0][u] = AGENT ? ld_agent(pu) : *pu;
       }
-    }
-    float2 mlr[GPW];
+    };
 #pragma unroll
-    for (int r = 0; r < GPW; ++r) {
+    for (int u = 0; u < CH; ++u) load_o(u);
+    float2 mlr[GPW];
+    auto load_ml = [&](int r) {
       const int g = min(wv + 4 * r, G - 1);
       const float *ml = reinterpret_cast<const float *>(
           &a.ws_ml[((long long)(gs0 + min(c0 + lane, nsplit - 1)) * a.n_kv + h) * G + g]);
       mlr[r] = AGENT ? make_float2(ld_agent(ml), ld_agent(ml + 1)) : make_float2(ml[0], ml[1]);
-    }
+    };
+#pragma unroll
+    for (int r = 0; r < GPW; ++r) load_ml(r);
     __syncthreads();  // earlier round's readers of s_w / s_sc are done
 #pragma unroll
     for (int r = 0; r < GPW; ++r) {
@@ -232,7 +235,7 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
       const float mn = fmaxf(m_old, wave_max(m));
       const float w = lane < n ? fast_exp2(m - mn) : 0.f;
       const float ls = wave_sum(w * mlr[r].y);
-      s_w[g * CH + lane] = w;
+      if (lane < CH) s_w[g * CH + lane] = w;
       if (lane == 0) {
         const float sc = fast_exp2(m_old - mn);  // 0 on the first round
         s_sc[g] = sc;
@@ -331,6 +334,21 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     cs = ld4(a.cos_tab + (long long)pos * 64 + 4 * j);
     sn = ld4(a.sin_tab + (long long)pos * 64 + 4 * j);
   }
+  // The new token's raw key and value (fused append), ahead of the K/V
+  // batch: a load issued after it would hold this workgroup's first dot
+  // product until the whole batch had arrived.
+  const bool fused = a.k_new != nullptr;
+  const bool own_pos = fused && pos >= t0 && pos < t1;
+  const bool need_new = fused && (own_pos || (a.k_rot && s == 0));
+  float4 nklo = make_float4(0.f, 0.f, 0.f, 0.f), nkhi = nklo, nvlo = nklo, nvhi = nklo;
+  if (need_new) {
+    const float *kn = a.k_new + b * a.kn_bstride + h * D;
+    const float *vn = a.v_new + b * a.kn_bstride + h * D;
+    nklo = ld4(kn + 4 * j);
+    nkhi = ld4(kn + 64 + 4 * j);
+    nvlo = ld4(vn + 4 * j);
+    nvhi = ld4(vn + 64 + 4 * j);
+  }
   float4 klo[RPG], khi[RPG], vlo[RPG], vhi[RPG];
   bool valid[RPG];
   auto load_pass = [&](int tp) {
@@ -370,16 +388,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
     qhi[g] = scale4(a.scale_log2, qhi[g]);
   }
 
-  // ---- the new token's rotated key and value (fused append) ----
-  const bool fused = a.k_new != nullptr;
-  float4 nklo = make_float4(0.f, 0.f, 0.f, 0.f), nkhi = nklo, nvlo = nklo, nvhi = nklo;
-  const bool own_pos = fused && pos >= t0 && pos < t1;
-  if (fused && (own_pos || (a.k_rot && s == 0))) {
-    const float *kn = a.k_new + b * a.kn_bstride + h * D;
-    const float *vn = a.v_new + b * a.kn_bstride + h * D;
-    rot4(ld4(kn + 4 * j), ld4(kn + 64 + 4 * j), cs, sn, nklo, nkhi);
-    nvlo = ld4(vn + 4 * j);
-    nvhi = ld4(vn + 64 + 4 * j);
+  // ---- the new token's rotated key (fused append) ----
+  if (need_new) {
+    rot4(nklo, nkhi, cs, sn, nklo, nkhi);
     if (a.k_rot && s == 0 && rg == 0) {
       float *kr = a.k_rot + b * a.kn_bstride + h * D;
       st4(kr + 4 * j, nklo);
@@ -484,7 +495,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   __syncthreads();
 
   const int gs = a.split_off[b] + s;  // global split index
-  for (int e = tid; e < G * D; e += 256) {
+  // This split's unnormalised output element e (q head e / D, dim e % D).
+  auto split_out = [&](int e) {
     const int g = e / D, dim = e % D;
     float O = 0.f;
 #pragma unroll
@@ -495,22 +507,31 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
       O = fmaf(w4.z, s_o[4 * r4 + 2][g][dim], O);
       O = fmaf(w4.w, s_o[4 * r4 + 3][g][dim], O);
     }
-    const float M = s_M[g], Ls = s_L[g];
-    if (nsplit == 1) {
-      a.out[b * a.out_bstride + ((long long)h * G + g) * D + dim] = O / Ls;
-    } else if (INLINE) {
-      st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], O);
-      if (dim == 0) {
-        float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + g]);
-        st_agent(ml, M);
-        st_agent(ml + 1, Ls);
+    return O;
+  };
+  if (nsplit == 1 || !INLINE) {
+    for (int e = tid; e < G * D; e += 256) {
+      const int g = e / D, dim = e % D;
+      const float O = split_out(e);
+      if (nsplit == 1) {
+        a.out[b * a.out_bstride + ((long long)h * G + g) * D + dim] = O / s_L[g];
+      } else {
+        a.ws_o[((long long)gs * a.n_kv + h) * G * D + e] = O;
+        if (dim == 0) a.ws_ml[((long long)gs * a.n_kv + h) * G + g] = make_float2(s_M[g], s_L[g]);
       }
-    } else {
-      a.ws_o[((long long)gs * a.n_kv + h) * G * D + e] = O;
-      if (dim == 0) a.ws_ml[((long long)gs * a.n_kv + h) * G + g] = make_float2(M, Ls);
+    }
+    return;
+  }
+
+  for (int e = tid; e < G * D; e += 256) {
+    st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], split_out(e));
+    if (e % D == 0) {
+      const int g = e / D;
+      float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + g]);
+      st_agent(ml, s_M[g]);
+      st_agent(ml + 1, s_L[g]);
     }
   }
-  if (nsplit == 1 || !INLINE) return;
 
   // ---- ticket: the last workgroup of this (sequence, kv head) merges ----
   __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
@@ -525,7 +546,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   if (!s_last) return;
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  merge_splits<G, true>(a, b, h, nsplit, &s_o[0][0][0]);
+  // Rounds of at most 32 splits keep the merge's registers below the
+  // kernel's own budget.
+  if (nsplit <= 16)
+    merge_splits<G, true, 16>(a, b, h, nsplit, &s_o[0][0][0]);
+  else
+    merge_splits<G, true, 32>(a, b, h, nsplit, &s_o[0][0][0]);
 }
 
 // Second kernel of the two-launch decode: one workgroup of 256 lanes per
@@ -672,146 +698,153 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // one: two of its workgroups fill LDS.)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Wpass-failed"
-template <int G>
-__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
-void prefill_kernel(PrefillArgs a) {
-  constexpr int D = kHeadDim, BQ = 32, BK = 32;
-  constexpr int TILE = BK * D;            // floats per K (or V) tile
-  constexpr int NI = TILE / 4 / (64 * G); // 1 KB copies per wave per tile
-  __shared__ __attribute__((aligned(16))) float sK0[TILE];
-  __shared__ __attribute__((aligned(16))) float sK1[TILE];
-  __shared__ __attribute__((aligned(16))) float sV0[TILE];
-  __shared__ __attribute__((aligned(16))) float sV1[TILE];
+constexpr int kPrefillTile = 32 * kHeadDim;  // floats per K (or V) tile
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = wave;
-  const int hl = lane >> 5, col = lane & 31;
-  const int h = blockIdx.x;  // kv head is the fastest grid axis
+// A prefill work item: kv head h, item y -> (query tile qt, key chunk ch of
+// nch), key tiles kt0 .. nkt-1.  Items run over query tiles from the last
+// (most keys) down, chunks of a tile consecutive, so long work comes first.
+struct PfItem {
+  int h, y, qt, ch, nch, q0, kt0, nkt;
+};
+
+__device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
+  PfItem it;
+  it.h = h;
+  it.y = y;
   const int last_row = a.start_pos + a.n_tokens - 1;
-  // blockIdx.y -> (query tile qt, chunk ch): query tiles from the last (most
-  // keys) down, chunks of a tile consecutive, so long work is dispatched first.
-  const int csh = a.chunk_shift, ctiles = 1 << csh;
-  int qt, ch, nch;
-  prefill_item(blockIdx.y, a.n_qtiles, a.start_pos, last_row, csh, qt, ch, nch);
-  const int q0 = qt * BQ;
-  const int qrow = min(q0 + col, a.n_tokens - 1);  // rows past the end are not stored
-  const int head = h * G + g;
-  const int pq = a.start_pos + qrow;               // this lane's query position
-  const int kmax = min(a.start_pos + q0 + BQ - 1, last_row);
-  const int kt0 = ch << csh;
-  const int nkt = min(kmax / BK + 1, kt0 + ctiles);  // key tiles kt0 .. nkt-1
+  prefill_item(y, a.n_qtiles, a.start_pos, last_row, a.chunk_shift, it.qt, it.ch, it.nch);
+  it.q0 = it.qt * 32;
+  const int kmax = min(a.start_pos + it.q0 + 31, last_row);
+  it.kt0 = it.ch << a.chunk_shift;
+  it.nkt = min(kmax / 32 + 1, it.kt0 + (1 << a.chunk_shift));
+  return it;
+}
+
+// Copy of key tile kt of kv head h: copy j of wave w fills rows 2J, 2J+1
+// (J = w*NI + j); lane l takes row 2J + l/32, LDS chunk l%32.  Rows past the
+// last cached one repeat it (their keys are masked for every query).
+template <int G>
+__device__ __forceinline__ void pf_copy_tile(const PrefillArgs &a, int h, int kt, float *dk,
+                                             float *dv) {
+  constexpr int NI = kPrefillTile / 4 / (64 * G);  // 1 KB copies per wave per tile
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int last_row = a.start_pos + a.n_tokens - 1;
   const float *kc = a.k_cache + h * a.kv_stride;
   const float *vc = a.v_cache + h * a.kv_stride;
-
-  // Copy of key tile kt: copy j of wave w fills rows 2J, 2J+1 (J = w*NI + j);
-  // lane l takes row 2J + l/32, LDS chunk l%32.  Rows past the last cached
-  // one repeat it (their keys are masked for every query).
-  auto copy_tile = [&](int kt, float *dk, float *dv) {
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int J = wave * NI + j;
-      const int r = 2 * J + hl, p = col;
-      const long long grow = (long long)min(kt * BK + r, last_row) * D;
-      dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
-      dma16(vc + grow + 4 * p, dv + J * 256);
-    }
-  };
-  copy_tile(kt0, sK0, sV0);
-
-  float qf[64];
-  {
-    const float *qp = a.q + ((long long)qrow * a.n_heads + head) * D + 64 * hl;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float4 v = ld4(qp + 4 * i);
-      qf[4 * i] = v.x * a.scale_log2;
-      qf[4 * i + 1] = v.y * a.scale_log2;
-      qf[4 * i + 2] = v.z * a.scale_log2;
-      qf[4 * i + 3] = v.w * a.scale_log2;
-    }
+  for (int j = 0; j < NI; ++j) {
+    const int J = wave * NI + j;
+    const int r = 2 * J + hl, p = col;
+    const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
+    dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
+    dma16(vc + grow + 4 * p, dv + J * 256);
   }
-  wait_vmem();
-  __syncthreads();
+}
 
-  floatx16 O[4];
+// This lane's Q fragment (dims 64*hl .. 64*hl+63 of its query, the wave's
+// head), unscaled.
+template <int G>
+__device__ __forceinline__ void pf_load_q(const PrefillArgs &a, const PfItem &it, float (&qf)[64]) {
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qrow = min(it.q0 + col, a.n_tokens - 1);  // rows past the end are not stored
+  const float *qp = a.q + ((long long)qrow * a.n_heads + it.h * G + g) * kHeadDim + 64 * hl;
 #pragma unroll
-  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
-  // m starts finite: in a chunk that is not the first, a query may see no key
-  // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
-  float m = -1e30f, l = 0.f;
+  for (int i = 0; i < 16; ++i) {
+    const float4 v = ld4(qp + 4 * i);
+    qf[4 * i] = v.x;
+    qf[4 * i + 1] = v.y;
+    qf[4 * i + 2] = v.z;
+    qf[4 * i + 3] = v.w;
+  }
+}
 
-  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv) {
-    if (kt + 1 < nkt) copy_tile(kt + 1, nk, nv);
+__device__ __forceinline__ void pf_scale_q(float (&qf)[64], float sc) {
+#pragma unroll
+  for (int i = 0; i < 64; ++i) qf[i] *= sc;
+}
 
-    // S^T tile: 32 keys x 32 queries.
-    floatx16 S = floatx16{};
-    const float *krow = dk + col * D + 64 * hl;
-    const int sw = col & 15;
+// S^T tile = K Q^T: 32 keys x 32 queries.
+__device__ __forceinline__ floatx16 pf_tile_s(const float *dk, const float (&qf)[64]) {
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  floatx16 S = floatx16{};
+  const float *krow = dk + col * kHeadDim + 64 * hl;
+  const int sw = col & 15;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float4 kv = ld4(krow + 4 * (i ^ sw));
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * i], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * i + 1], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * i + 2], S, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
-    }
-    const int kbase = kt * BK;
-    if (kbase + BK - 1 > a.start_pos + q0) {  // the tile reaches the causal diagonal
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kbase + 8 * (r >> 2) + 4 * hl + (r & 3);
-        if (key > pq) S[r] = -INFINITY;
-      }
-    }
-    float mb = S[0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) mb = fmaxf(mb, S[r]);
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
-    // Lazy rescaling: m is the reference the exponentials are taken against;
-    // it moves only when a query's max exceeds it by more than 8 (so every
-    // p <= 2^8).  O lives in accumulation registers, so a rescale is costly
-    // and is skipped for the whole wave when no lane needs it.  The first
-    // tile with a visible key sets m.
-    if (__ballot(mb > m + 8.0f) != 0) {
-      const float mn = fmaxf(m, mb);
-      const float alpha = fast_exp2(m - mn);
-      l *= alpha;
-#pragma unroll
-      for (int db = 0; db < 4; ++db) O[db] *= alpha;
-      m = mn;
-    }
-    float p[16], ls = 0.f;
+  for (int i = 0; i < 16; ++i) {
+    const float4 kv = ld4(krow + 4 * (i ^ sw));
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * i], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * i + 1], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * i + 2], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
+  }
+  return S;
+}
+
+// Causal mask, online softmax and O^T += V^T P^T for key tile kt.
+__device__ __forceinline__ void pf_tile_pv(const PrefillArgs &a, const PfItem &it, int kt,
+                                           floatx16 S, const float *dv, floatx16 (&O)[4],
+                                           float &m, float &l) {
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  const int kbase = kt * 32;
+  if (kbase + 31 > a.start_pos + it.q0) {  // the tile reaches the causal diagonal
+    const int pq = a.start_pos + min(it.q0 + col, a.n_tokens - 1);  // this lane's query position
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = fast_exp2(S[r] - m);
-      ls += p[r];
+      const int key = kbase + 8 * (r >> 2) + 4 * hl + (r & 3);
+      if (key > pq) S[r] = -INFINITY;
     }
-    l += ls;
-
-    // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile.
-#pragma unroll
-    for (int s = 0; s < 16; ++s) {
-      const float4 vv = ld4(dv + (8 * (s >> 2) + 4 * hl + (s & 3)) * D + 4 * col);
-      O[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, p[s], O[0], 0, 0, 0);
-      O[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, p[s], O[1], 0, 0, 0);
-      O[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[s], O[2], 0, 0, 0);
-      O[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[s], O[3], 0, 0, 0);
-    }
-    wait_vmem();  // this wave's copies of the next tile have landed
-    __syncthreads();
-  };
-  for (int kt = kt0;;) {
-    step(kt, sK0, sV0, sK1, sV1);
-    if (++kt >= nkt) break;
-    step(kt, sK1, sV1, sK0, sV0);
-    if (++kt >= nkt) break;
   }
+  float mb = S[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mb = fmaxf(mb, S[r]);
+  mb = fmaxf(mb, __shfl_xor(mb, 32));
+  // Lazy rescaling: m is the reference the exponentials are taken against;
+  // it moves only when a query's max exceeds it by more than 8 (so every
+  // p <= 2^8).  O lives in accumulation registers, so a rescale is costly
+  // and is skipped for the whole wave when no lane needs it.  The first
+  // tile with a visible key sets m.
+  if (__ballot(mb > m + 8.0f) != 0) {
+    const float mn = fmaxf(m, mb);
+    const float alpha = fast_exp2(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) O[db] *= alpha;
+    m = mn;
+  }
+  float p[16], ls = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    p[r] = fast_exp2(S[r] - m);
+    ls += p[r];
+  }
+  l += ls;
+  // O^T += V^T P^T: step s takes key row 8*(s/4) + 4*hl + s%4 of the tile.
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float4 vv = ld4(dv + (8 * (s >> 2) + 4 * hl + (s & 3)) * kHeadDim + 4 * col);
+    O[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, p[s], O[0], 0, 0, 0);
+    O[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, p[s], O[1], 0, 0, 0);
+    O[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, p[s], O[2], 0, 0, 0);
+    O[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, p[s], O[3], 0, 0, 0);
+  }
+}
 
-  if (nch > 1) {
+// End of an item: a chunk of a split query tile stores its partial state and
+// takes a ticket; the last chunk to finish merges the others into its own
+// registers and, like an unsplit item, writes the output.
+template <int G>
+__device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it,
+                                          floatx16 (&O)[4], float m, float l, int *s_last) {
+  const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, col = lane & 31;
+  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = it.h, head = h * G + g;
+  if (it.nch > 1) {
     // Partial state of this chunk, lane-coalesced: component c (0..63 O, 64 m,
     // 65 l) of lane `lane` of wave g at ws[((item * G + g) * 66 + c) * 64 + lane].
-    const int item0 = blockIdx.y - ch;  // first chunk of this query tile
-    float *slot = a.ws + (((long long)h * a.n_items + blockIdx.y) * G + g) * 66 * 64 + lane;
+    const int item0 = it.y - it.ch;  // first chunk of this query tile
+    float *slot = a.ws + (((long long)h * a.n_items + it.y) * G + g) * 66 * 64 + lane;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -820,19 +853,20 @@ void prefill_kernel(PrefillArgs a) {
     st_agent(slot + 65 * 64, l);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
     __syncthreads();
-    __shared__ int s_last;
-    unsigned *ctr = a.counters + ((long long)h * a.n_qtiles + qt) * kCounterStride;
+    unsigned *ctr = a.counters + ((long long)h * a.n_qtiles + it.qt) * kCounterStride;
     if (tid == 0) {
       const unsigned ticket =
           __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = ticket == (unsigned)(nch - 1);
+      *s_last = ticket == (unsigned)(it.nch - 1);
     }
     __syncthreads();
-    if (!s_last) return;
+    const bool last = *s_last;
+    __syncthreads();  // s_last is read before the next item may write it
+    if (!last) return;
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Merge the other chunks into this one's registers (same lane layout).
-    for (int c = 0; c < nch; ++c) {
-      if (c == ch) continue;
+    for (int c = 0; c < it.nch; ++c) {
+      if (c == it.ch) continue;
       const float *src = a.ws + (((long long)h * a.n_items + item0 + c) * G + g) * 66 * 64 + lane;
       float ov[64];
 #pragma unroll
@@ -850,12 +884,149 @@ void prefill_kernel(PrefillArgs a) {
   }
   // Lane (col, hl) holds, for r = 4*rq + r3, dims 32*rq + 16*hl + 4*r3 + db.
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
-  if (q0 + col < a.n_tokens) {
-    float *op = a.out + ((long long)(q0 + col) * a.n_heads + head) * D + 16 * hl;
+  if (it.q0 + col < a.n_tokens) {
+    float *op = a.out + ((long long)(it.q0 + col) * a.n_heads + head) * kHeadDim + 16 * hl;
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       st4(op + 32 * (r >> 2) + 4 * (r & 3),
           make_float4(O[0][r] * inv, O[1][r] * inv, O[2][r] * inv, O[3][r] * inv));
+  }
+}
+
+// Grid-mapped prefill: workgroup (h = blockIdx.x, y = blockIdx.y), kv head
+// the fastest axis, so the longest items of every head are dispatched first.
+// The four LDS tile buffers are separate arrays so that the compiler can
+// tell a read of the current tile from the copy of the next one in flight.
+template <int G>
+__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) float sK0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sK1[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV1[kPrefillTile];
+  __shared__ int s_last;
+  const PfItem it = pf_item(a, blockIdx.x, blockIdx.y);
+  pf_copy_tile<G>(a, it.h, it.kt0, sK0, sV0);
+  float qf[64];
+  pf_load_q<G>(a, it, qf);
+  pf_scale_q(qf, a.scale_log2);
+  wait_vmem();
+  __syncthreads();
+  floatx16 O[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+  // m starts finite: in a chunk that is not the first, a query may see no key
+  // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
+  float m = -1e30f, l = 0.f;
+  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv) {
+    if (kt + 1 < it.nkt) pf_copy_tile<G>(a, it.h, kt + 1, nk, nv);
+    const floatx16 S = pf_tile_s(dk, qf);
+    pf_tile_pv(a, it, kt, S, dv, O, m, l);
+    wait_vmem();  // this wave's copies of the next tile have landed
+    __syncthreads();
+  };
+  for (int kt = it.kt0;;) {
+    step(kt, sK0, sV0, sK1, sV1);
+    if (++kt >= it.nkt) break;
+    step(kt, sK1, sV1, sK0, sV0);
+    if (++kt >= it.nkt) break;
+  }
+  pf_finish<G>(a, it, O, m, l, &s_last);
+}
+
+// Persistent prefill: gridDim.x resident workgroups (at most the number of
+// items) start on item blockIdx.x and take further items (kv head fastest,
+// longest first) from an atomic queue.  The next item's index is taken
+// during the current item's first tile; during its last tile the next
+// item's first K/V tile is copied into the free buffer pair and, once the
+// tile's products have read the Q fragment, the next Q fragment is loaded,
+// so a workgroup's start-up latency runs under the previous item's work.
+// (After a one-tile item the successor is loaded without overlap: its index
+// arrives with that tile.)  Tiles alternate between the two buffer pairs
+// across item boundaries; the loop body is unrolled over the pair so that
+// each buffer is named statically (the compiler can tell the copy in flight
+// from the tile being read).  A workgroup leaves once its queue index passes
+// the last item; the last to leave resets the queue for the next launch.
+template <int G>
+__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_persistent_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) float sK0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sK1[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV1[kPrefillTile];
+  __shared__ int s_last, s_item[2];
+  const int tid = threadIdx.x;
+  const int total = a.n_kv * a.n_items;
+  unsigned *next = a.queue, *left = a.queue + kCounterStride;
+  auto item = [&](int y) { return pf_item(a, y % a.n_kv, y / a.n_kv); };
+  PfItem it = item(blockIdx.x);
+  pf_copy_tile<G>(a, it.h, it.kt0, sK0, sV0);
+  float qf[64];
+  pf_load_q<G>(a, it, qf);
+  pf_scale_q(qf, a.scale_log2);
+  wait_vmem();
+  __syncthreads();
+  floatx16 O[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+  float m = -1e30f, l = 0.f;
+  int kt = it.kt0, par = 0;
+  int nxt = total;  // the next item, once its index has arrived
+  // One tile on (dk, dv); the next tile of this item, or the next item's
+  // first, is copied into (nk, nv).  Returns false once the workgroup has no
+  // item left.
+  auto step = [&](const float *dk, const float *dv, float *nk, float *nv) -> bool {
+    const bool first = kt == it.kt0, lastt = kt + 1 == it.nkt;
+    const bool pre = lastt && nxt < total;
+    PfItem nit = pre ? item(nxt) : it;
+    if (!lastt || pre) pf_copy_tile<G>(a, lastt ? nit.h : it.h, lastt ? nit.kt0 : kt + 1, nk, nv);
+    int ticket = 0;
+    if (first && tid == 0)  // in flight during this tile
+      ticket = (int)gridDim.x +
+               (int)__hip_atomic_fetch_add(next, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const floatx16 S = pf_tile_s(dk, qf);
+    pf_tile_pv(a, it, kt, S, dv, O, m, l);
+    if (pre) pf_load_q<G>(a, nit, qf);  // qf is no longer read by this item
+    if (first && tid == 0) s_item[par] = ticket;
+    if (lastt) pf_finish<G>(a, it, O, m, l, &s_last);
+    wait_vmem();  // this wave's copies (next tile, next Q) have landed
+    __syncthreads();
+    // The slot alternates with the item: a rewrite of one slot comes after
+    // the following item's first barrier, which every reader has passed.
+    if (first) nxt = __builtin_amdgcn_readfirstlane(s_item[par]);
+    if (!lastt) {
+      ++kt;
+      return true;
+    }
+    if (nxt >= total) return false;
+    if (!pre) {  // one-tile item: the successor was not known in time
+      nit = item(nxt);
+      pf_copy_tile<G>(a, nit.h, nit.kt0, nk, nv);
+      pf_load_q<G>(a, nit, qf);
+      wait_vmem();
+      __syncthreads();
+    }
+    it = nit;
+    kt = it.kt0;
+    nxt = total;
+    par ^= 1;
+    pf_scale_q(qf, a.scale_log2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+    m = -1e30f;
+    l = 0.f;
+    return true;
+  };
+  for (;;) {
+    if (!step(sK0, sV0, sK1, sV1)) break;
+    if (!step(sK1, sV1, sK0, sV0)) break;
+  }
+  if (tid == 0) {
+    const unsigned out = __hip_atomic_fetch_add(left, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (out == gridDim.x - 1) {  // every workgroup has taken its last index
+      __hip_atomic_store(next, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(left, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 #pragma clang diagnostic pop
@@ -980,8 +1151,19 @@ PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift) {
   return p;
 }
 
-hipError_t launch_prefill(const PrefillArgs &a, int group, hipStream_t s) {
+hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, hipStream_t s) {
   if (a.n_tokens <= 0) return hipSuccess;
+  if (persistent_wgs > 0) {
+    if (!a.queue) return hipErrorInvalidValue;
+    const dim3 grid(persistent_wgs);
+    switch (group) {
+      case 2: prefill_persistent_kernel<2><<<grid, dim3(128), 0, s>>>(a); break;
+      case 4: prefill_persistent_kernel<4><<<grid, dim3(256), 0, s>>>(a); break;
+      case 8: prefill_persistent_kernel<8><<<grid, dim3(512), 0, s>>>(a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid(a.n_kv, a.n_items);
   switch (group) {
     case 2: prefill_kernel<2><<<grid, dim3(128), 0, s>>>(a); break;

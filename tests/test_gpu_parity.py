@@ -343,18 +343,20 @@ def test_dev_prefill_shapes(backend, n_heads, n_kv, n_tokens, start):
     assert_close(host(out), out_ref, f"prefill {n_heads}/{n_kv} n {n_tokens}")
 
 
-@pytest.mark.parametrize("shift", [0, 1, 3])
-def test_dev_prefill_key_chunks(monkeypatch, shift):
+@pytest.mark.parametrize("shift,persistent", [(0, 0), (1, 0), (3, 0), (1, 1), (3, 1), (20, 1)])
+def test_dev_prefill_key_chunks(monkeypatch, shift, persistent):
     """Query tiles cut into key chunks of 2^shift tiles (merged by the last
     chunk to finish), at start positions that are not tile-aligned so some
     chunks see no key at all for their first queries; two prefills in a row
-    check that the merge tickets reset themselves."""
-    case(f"prefill key chunks shift {shift}")
+    check that the merge tickets (and, persistent, the item queue) reset
+    themselves.  persistent: resident workgroups take items from a queue."""
+    case(f"prefill key chunks shift {shift} persistent {persistent}")
     import torch
 
     import bitnetrs_amd
 
     monkeypatch.setenv("BNR_PREFILL_CHUNK_SHIFT", str(shift))
+    monkeypatch.setenv("BNR_PREFILL_PERSISTENT", str(persistent))
     be_gpu = bitnetrs_amd.HipBackend(0)
     try:
         cap = 640
