@@ -88,10 +88,109 @@ struct PrefillArgs {
   int chunk_shift;
   int n_qtiles;                      // ceil(n_tokens / 32)
   int n_items;                       // (query tile, chunk) items per kv head
-  float *ws;                         // partial states: [n_kv][n_items][G][66][64]
+  float *ws;                         // partial states: [n_kv][n_items][G][66][64], by (query tile, chunk)
   unsigned *counters;                // [n_kv][n_qtiles] x kCounterStride, zero between launches
   unsigned *queue;                   // persistent launch: next item, workgroups done (2 x kCounterStride), zero between launches
+  // Item order (prefill_order fills these).  lpt: longest first -- every
+  // full-length chunk (n_full of them per kv head), then the shorter last
+  // chunks of the query tiles by decreasing length, those of length ct-1-b
+  // at part_off[b] .. part_off[b+1]-1 after the full ones (ct = 2^chunk_shift
+  // <= kMaxLptChunk).  Otherwise query tiles from the last down, the chunks
+  // of one tile consecutive.
+  int lpt, n_full;
+  int part_off[64];
 };
+constexpr int kMaxLptChunk = 64;
+
+// Sum over x = 1..m of floor(x / 2^sh), and of ceil(x / 2^sh) (m >= 0).
+__host__ __device__ inline long long pf_floor_sum(long long m, int sh) {
+  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
+  return q > 0 ? (((q * (q - 1)) >> 1) << sh) + q * (r + 1) : 0;
+}
+__host__ __device__ inline long long pf_ceil_sum(long long m, int sh) {
+  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
+  return ((q * (q + 1) >> 1) << sh) + r * (q + 1);
+}
+
+// Work item y (per kv head) of a prefill launch -> query tile qt, chunk ch
+// of its nch chunks, and base = the partial-state slot of the tile's chunk
+// 0 (slot of chunk ch: base + ch).  Query tile qt < nqt-1 has qt + A key
+// tiles, A = ceil((start_pos + 1) / 32); the last (possibly short) tile
+// last_row / 32 + 1.  The host's dispatch replay uses the same function.
+__host__ __device__ inline void prefill_map(const PrefillArgs &a, int y, int &qt, int &ch,
+                                            int &nch, int &base) {
+  const int sh = a.chunk_shift, ct = 1 << sh, nqt = a.n_qtiles;
+  const int last_row = a.start_pos + a.n_tokens - 1;
+  const int A = (a.start_pos + 31) / 32 + 1;
+  const int nt_last = last_row / 32 + 1;
+  if (!a.lpt) {
+    // Tiles from the last down, chunks consecutive: the items of tiles
+    // q .. nqt-2 are a difference of two ceil sums; binary search.
+    const int nch_last = (nt_last + ct - 1) >> sh;
+    if (y < nch_last) {
+      qt = nqt - 1;
+      ch = y;
+      nch = nch_last;
+    } else {
+      const long long yy = y - nch_last;
+      const long long top = pf_ceil_sum(nqt - 2 + A, sh);
+      int lo = 0, hi = nqt - 2;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (top - pf_ceil_sum(mid - 1 + A, sh) > yy) lo = mid;
+        else hi = mid - 1;
+      }
+      qt = lo;
+      ch = (int)(yy - (top - pf_ceil_sum(lo + A, sh)));
+      nch = (lo + A + ct - 1) >> sh;
+    }
+  } else if (y < a.n_full) {
+    // Full chunks: the last tile's, then tiles nqt-2 down to 0 (floor sums).
+    const int f_last = nt_last >> sh;
+    if (y < f_last) {
+      qt = nqt - 1;
+      ch = y;
+      nch = (nt_last + ct - 1) >> sh;
+    } else {
+      const long long yy = y - f_last;
+      const long long top = pf_floor_sum(nqt - 2 + A, sh);
+      int lo = 0, hi = nqt - 2;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (top - pf_floor_sum(mid - 1 + A, sh) > yy) lo = mid;
+        else hi = mid - 1;
+      }
+      qt = lo;
+      ch = (int)(yy - (top - pf_floor_sum(lo + A, sh)));
+      nch = (lo + A + ct - 1) >> sh;
+    }
+  } else {
+    // Last chunks shorter than ct, longest first; within one length the
+    // last tile first, then the others from the highest tile down.
+    const int y2 = y - a.n_full;
+    int b = 0;
+    while (b + 1 < ct - 1 && a.part_off[b + 1] <= y2) ++b;
+    const int r = ct - 1 - b;
+    int k = y2 - a.part_off[b];
+    if ((nt_last & (ct - 1)) == r) {
+      if (k == 0) {
+        qt = nqt - 1;
+        ch = nt_last >> sh;
+        nch = ch + 1;
+        base = (int)(pf_ceil_sum(qt - 1 + A, sh) - pf_ceil_sum(A - 1, sh));
+        return;
+      }
+      --k;
+    }
+    const int q0 = ((r - A) % ct + ct) % ct;  // lowest regular tile with qt + A = r (mod ct)
+    const int cnt = nqt - 2 >= q0 ? (nqt - 2 - q0) / ct + 1 : 0;
+    qt = q0 + (cnt - 1 - k) * ct;
+    ch = (qt + A) >> sh;
+    nch = ch + 1;
+  }
+  base = (int)(pf_ceil_sum(qt - 1 + A, sh) - pf_ceil_sum(A - 1, sh));
+}
+
 // (query tile, chunk) items per kv head of a prefill launch, and the key
 // tiles they cover in total.
 struct PrefillPlan {
@@ -100,6 +199,9 @@ struct PrefillPlan {
   bool split;  // some query tile has more than one chunk
 };
 PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift);
+// Fills a.lpt, a.n_full and a.part_off from a.n_tokens, a.start_pos,
+// a.n_qtiles and a.chunk_shift.
+void prefill_order(PrefillArgs &a);
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.
 hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, hipStream_t s);
 bool prefill_supported(int group);

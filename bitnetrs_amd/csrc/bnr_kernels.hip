@@ -654,43 +654,6 @@ __device__ __forceinline__ void dma16(const float *g, float *lds) {
   __builtin_amdgcn_global_load_lds((global_void_t *)g, (lds_void_t *)lds, 16, 0, 0);
 }
 
-// Sum over x = 1..m of ceil(x / 2^sh).
-__device__ __forceinline__ long long ceil_sum(long long m, int sh) {
-  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
-  return ((q * (q + 1) >> 1) << sh) + r * (q + 1);
-}
-
-// Work item y of a prefill launch -> (query tile qt, chunk ch of nch).  Items
-// run over query tiles from the last down, chunks of a tile consecutive.  The
-// last tile may be short; every other tile qt has qt + A key tiles with
-// A = ceil((start_pos + 1) / 32) (its last query sits at start_pos + 32 qt + 31),
-// so the items of tiles q .. nqt-2 are a difference of two ceil sums and the
-// tile of item y is found by binary search.
-__device__ __forceinline__ void prefill_item(int y, int nqt, int start_pos, int last_row, int sh,
-                                             int &qt, int &ch, int &nch) {
-  const int ct = 1 << sh;
-  const int nch_last = (last_row / 32 + 1 + ct - 1) >> sh;
-  if (y < nch_last) {
-    qt = nqt - 1;
-    ch = y;
-    nch = nch_last;
-    return;
-  }
-  const long long yy = y - nch_last;
-  const int A = (start_pos + 31) / 32 + 1;
-  const long long top = ceil_sum(nqt - 2 + A, sh);
-  // items of tiles q .. nqt-2: top - ceil_sum(q - 1 + A); largest q with more than yy
-  int lo = 0, hi = nqt - 2;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (top - ceil_sum(mid - 1 + A, sh) > yy) lo = mid;
-    else hi = mid - 1;
-  }
-  qt = lo;
-  ch = (int)(yy - (top - ceil_sum(lo + A, sh)));
-  nch = (lo + A + ct - 1) >> sh;
-}
-
 // s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -701,10 +664,10 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 constexpr int kPrefillTile = 32 * kHeadDim;  // floats per K (or V) tile
 
 // A prefill work item: kv head h, item y -> (query tile qt, key chunk ch of
-// nch), key tiles kt0 .. nkt-1.  Items run over query tiles from the last
-// (most keys) down, chunks of a tile consecutive, so long work comes first.
+// nch), key tiles kt0 .. nkt-1, partial-state slot of the tile's chunk 0
+// (base).  The order of the items is prefill_map's.
 struct PfItem {
-  int h, y, qt, ch, nch, q0, kt0, nkt;
+  int h, y, qt, ch, nch, base, q0, kt0, nkt;
 };
 
 __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
@@ -712,7 +675,7 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
   it.h = h;
   it.y = y;
   const int last_row = a.start_pos + a.n_tokens - 1;
-  prefill_item(y, a.n_qtiles, a.start_pos, last_row, a.chunk_shift, it.qt, it.ch, it.nch);
+  prefill_map(a, y, it.qt, it.ch, it.nch, it.base);
   it.q0 = it.qt * 32;
   const int kmax = min(a.start_pos + it.q0 + 31, last_row);
   it.kt0 = it.ch << a.chunk_shift;
@@ -843,8 +806,7 @@ __device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it
   if (it.nch > 1) {
     // Partial state of this chunk, lane-coalesced: component c (0..63 O, 64 m,
     // 65 l) of lane `lane` of wave g at ws[((item * G + g) * 66 + c) * 64 + lane].
-    const int item0 = it.y - it.ch;  // first chunk of this query tile
-    float *slot = a.ws + (((long long)h * a.n_items + it.y) * G + g) * 66 * 64 + lane;
+    float *slot = a.ws + (((long long)h * a.n_items + it.base + it.ch) * G + g) * 66 * 64 + lane;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -867,7 +829,7 @@ __device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it
     // Merge the other chunks into this one's registers (same lane layout).
     for (int c = 0; c < it.nch; ++c) {
       if (c == it.ch) continue;
-      const float *src = a.ws + (((long long)h * a.n_items + item0 + c) * G + g) * 66 * 64 + lane;
+      const float *src = a.ws + (((long long)h * a.n_items + it.base + c) * G + g) * 66 * 64 + lane;
       float ov[64];
 #pragma unroll
       for (int i = 0; i < 64; ++i) ov[i] = ld_agent(src + i * 64);
@@ -1136,6 +1098,26 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
 }
 
 bool prefill_supported(int group) { return group == 2 || group == 4 || group == 8; }
+
+void prefill_order(PrefillArgs &a) {
+  const int sh = a.chunk_shift, ct = 1 << sh, nqt = a.n_qtiles;
+  const int last_row = a.start_pos + a.n_tokens - 1;
+  const int A = (a.start_pos + 31) / 32 + 1;
+  const int nt_last = last_row / 32 + 1;
+  a.lpt = ct <= kMaxLptChunk && ct > 1;
+  a.n_full = 0;
+  for (int b = 0; b < kMaxLptChunk; ++b) a.part_off[b] = 0;
+  if (!a.lpt) return;
+  int count[kMaxLptChunk] = {};  // last chunks of length r (< ct)
+  a.n_full = nt_last >> sh;
+  count[nt_last & (ct - 1)] += 1;
+  for (int qt = 0; qt + 1 < nqt; ++qt) {
+    a.n_full += (qt + A) >> sh;
+    count[(qt + A) & (ct - 1)] += 1;
+  }
+  // bucket b holds length ct-1-b; part_off[b] = items of longer buckets
+  for (int b = 1; b < ct; ++b) a.part_off[b] = a.part_off[b - 1] + count[ct - b];
+}
 
 PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift) {
   const int last_row = start_pos + n_tokens - 1, nqt = (n_tokens + 31) / 32;
