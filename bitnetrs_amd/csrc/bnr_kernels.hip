@@ -546,12 +546,16 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
   if (!s_last) return;
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // Rounds of at most 32 splits keep the merge's registers below the
-  // kernel's own budget.
+  // One round (one load round trip) for up to 64 splits, sized so that at
+  // most a quarter of the loads are clamped duplicates.
   if (nsplit <= 16)
     merge_splits<G, true, 16>(a, b, h, nsplit, &s_o[0][0][0]);
-  else
+  else if (nsplit <= 32)
     merge_splits<G, true, 32>(a, b, h, nsplit, &s_o[0][0][0]);
+  else if (nsplit <= 48)
+    merge_splits<G, true, 48>(a, b, h, nsplit, &s_o[0][0][0]);
+  else
+    merge_splits<G, true, 64>(a, b, h, nsplit, &s_o[0][0][0]);
 }
 
 // Second kernel of the two-launch decode: one workgroup of 256 lanes per
