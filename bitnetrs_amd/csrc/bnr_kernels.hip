@@ -290,7 +290,8 @@ __device__ __forceinline__ void merge_splits(const DecodeArgs &a, int b, int h, 
 // memset is needed between launches.
 // ---------------------------------------------------------------------------
 template <int G, int RPG, bool INLINE, bool RAGGED>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((RPG == 4 && !INLINE && G <= 4) ? 3 : 1)))
+void decode_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   __shared__ float s_o[16][G][D];
   __shared__ float s_m[G][16];
