@@ -1,6 +1,7 @@
 // bnr_kernels.hip -- gfx950 kernels of the GQA attention hot path.
 //
 //  rope_append_kernel  half-split RoPE of q/k + head-major KV append
+//                       (rope_append_vec_kernel: four pairs per thread)
 //  decode_kernel<G,RPG> split-K decode attention, head_dim 128, optional
 //                       fused RoPE + append, last-workgroup merge
 //  decode_generic_kernel any head_dim / group size
@@ -148,6 +149,45 @@ __device__ __forceinline__ float4 ld4(const float *p) {
 
 __device__ __forceinline__ void st4(float *p, float4 v) {
   *reinterpret_cast<float4 *>(p) = v;
+}
+
+// Four consecutive pairs (i .. i+3, i+half .. i+half+3) per thread, 16-byte
+// accesses: the same rotation as rope_append_kernel, element for element.
+// Needs half % 4 == 0 and 16-byte aligned rows and tables.
+__global__ __launch_bounds__(256) void rope_append_vec_kernel(RopeAppendArgs a) {
+  const int half = a.head_dim >> 1, quads = half >> 2;
+  const int slots = a.n_heads + 2 * a.n_kv;
+  const long long total = (long long)a.n_tokens * slots * quads;
+  for (long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int i = 4 * (int)(idx % quads);
+    const long long rest = idx / quads;
+    const int slot = (int)(rest % slots);
+    const int tok = (int)(rest / slots);
+    const int pos = a.start_pos + tok;
+    if (slot < a.n_heads + a.n_kv) {
+      const bool is_q = slot < a.n_heads;
+      float *x = is_q ? a.q + ((long long)tok * a.n_heads + slot) * a.head_dim
+                      : a.k + ((long long)tok * a.n_kv + (slot - a.n_heads)) * a.head_dim;
+      const float4 c = ld4(a.cos_tab + (long long)pos * half + i);
+      const float4 sn = ld4(a.sin_tab + (long long)pos * half + i);
+      float4 lo, hi;
+      rot4(ld4(x + i), ld4(x + i + half), c, sn, lo, hi);
+      st4(x + i, lo);
+      st4(x + i + half, hi);
+      if (!is_q && a.k_cache) {
+        float *dst = a.k_cache + (slot - a.n_heads) * a.kv_stride + (long long)pos * a.head_dim;
+        st4(dst + i, lo);
+        st4(dst + i + half, hi);
+      }
+    } else if (a.v_cache) {
+      const int hv = slot - a.n_heads - a.n_kv;
+      const float *src = a.v + ((long long)tok * a.n_kv + hv) * a.head_dim;
+      float *dst = a.v_cache + hv * a.kv_stride + (long long)pos * a.head_dim;
+      st4(dst + i, ld4(src + i));
+      st4(dst + i + half, ld4(src + i + half));
+    }
+  }
 }
 
 // Agent-coherent scalar store / load: performed at the device-wide coherence
@@ -1084,11 +1124,19 @@ hipError_t launch_decode_g(const DecodeArgs &a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s) {
-  const long long total = (long long)a.n_tokens * (a.n_heads + 2 * a.n_kv) * (a.head_dim / 2);
+  auto a16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+  const int half = a.head_dim / 2;
+  const bool vec = half % 4 == 0 && a16(a.q) && a16(a.k) && a16(a.cos_tab) && a16(a.sin_tab) &&
+                   (!a.v_cache || (a16(a.v) && a16(a.v_cache))) && (!a.k_cache || a16(a.k_cache)) &&
+                   a.kv_stride % 4 == 0;
+  const long long total = (long long)a.n_tokens * (a.n_heads + 2 * a.n_kv) * (vec ? half / 4 : half);
   if (total == 0) return hipSuccess;
   long long blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  rope_append_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a);
+  if (vec)
+    rope_append_vec_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a);
+  else
+    rope_append_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a);
   return hipGetLastError();
 }
 
