@@ -594,8 +594,8 @@ def main() -> int:
                     help="also run plain copies of a known size (for --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the attention path is single-GPU (see DESIGN.md for how it would shard)",
+        print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}); the attention "
+              "path runs on a single GPU and has no multi-GPU launch",
               file=sys.stderr)
         return 2
 

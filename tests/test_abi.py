@@ -67,7 +67,8 @@ def test_null_context_is_an_error_not_a_crash():
 
 
 def test_integration_rust_extern_block_matches_header():
-    # The Rust binding in INTEGRATION.md declares exactly the header's functions.
+    # The Rust extern block of the integration guide at the repository root
+    # declares exactly the header's functions.
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     block = text.split("extern \"C\" {", 1)[1].split("\n}\n", 1)[0]
     rust = sorted(set(re.findall(r"fn (bnr_\w+)\s*\(", block)))
