@@ -1496,6 +1496,9 @@ extern "C" int bnr_dev_ternary_gemv_norm_group(
   p.gamma = gamma;
   p.eps = eps;
   p.h_out = mode == BNR_GLUE_RESIDUAL ? h_out : nullptr;
+  // The vector path also reads the activation vectors as float4 groups.
+  vec = vec && in_features % 16 == 0 && aligned16(a) && aligned16(gamma) &&
+        (mode == BNR_GLUE_PLAIN || aligned16(b)) && (!p.h_out || aligned16(p.h_out));
   DeviceGuard dg(c->device);
   HIP_TRY(launch_ternary_gemv_norm(g, p, vec, (hipStream_t)stream), "ternary_gemv_norm launch");
   return set_ok();

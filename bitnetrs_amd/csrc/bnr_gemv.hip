@@ -55,6 +55,15 @@ __device__ __forceinline__ uint4 transpose_bytes(uint4 x) {
 }
 
 template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lanef(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
@@ -185,15 +194,36 @@ constexpr int kNormPieces = kNormK / 64;     // 16-byte weight pieces per row
 constexpr int kNormPiecesPerLane = kNormPieces / 16;
 constexpr int kNormGroupsPerThread = kNormGroups / 256;
 
-__device__ __forceinline__ float norm_x(const GemvNormArgs &p, int i) {
+// x from the glue inputs: a | a + b | max(a, 0)^2 * b (mode kGlue*).
+__device__ __forceinline__ float norm_x_of(int mode, float u, float v) {
 #pragma clang fp contract(off)
-  const float u = p.a[i];
-  if (p.mode == kGlueResidual) return u + p.b[i];
-  if (p.mode == kGlueSqrelu) {
+  if (mode == kGlueResidual) return u + v;
+  if (mode == kGlueSqrelu) {
     const float r = fmaxf(u, 0.0f);
-    return r * r * p.b[i];
+    return r * r * v;
   }
   return u;
+}
+
+__device__ __forceinline__ float norm_x(const GemvNormArgs &p, int i) {
+  return norm_x_of(p.mode, p.a[i], p.mode == kGluePlain ? 0.f : p.b[i]);
+}
+
+// Sum / max over the 64 lanes of a wave: DPP inside each 16-lane row, then
+// the four row results (the same order in every wave).
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v += dppf<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dppf<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dppf<0x141>(v);  // row_half_mirror
+  v += dppf<0x140>(v);  // row_mirror
+  return (lanef(v, 0) + lanef(v, 16)) + (lanef(v, 32) + lanef(v, 48));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = fmaxf(v, dppf<0xB1>(v));
+  v = fmaxf(v, dppf<0x4E>(v));
+  v = fmaxf(v, dppf<0x141>(v));
+  v = fmaxf(v, dppf<0x140>(v));
+  return fmaxf(fmaxf(lanef(v, 0), lanef(v, 16)), fmaxf(lanef(v, 32), lanef(v, 48)));
 }
 
 __device__ __forceinline__ float norm_y(float x, float inv, float g) {
@@ -235,29 +265,62 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
     else
       wq[i] = 16 * c < nb ? load16_bounded(w, b0 + 16 * c, b0 + nb) : make_uint4(0, 0, 0, 0);
   }
-  // 2. x for groups tid, tid+256 (16 consecutive elements each), sum of squares
+  // 2. x for groups tid, tid+256 (16 consecutive elements each), sum of
+  // squares.  VEC: K % 16 == 0 and 16-byte aligned vectors, so a group is
+  // four float4 loads of each input.
   float x[kNormGroupsPerThread][16], g[kNormGroupsPerThread][16];
   float ss = 0.f;
 #pragma unroll
   for (int q = 0; q < kNormGroupsPerThread; ++q) {
     const int e0 = 16 * (tid + 256 * q);
+    if (VEC) {
+      const bool in = e0 < K;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int i = e0 + e;
-      x[q][e] = i < K ? norm_x(p, i) : 0.f;
-      g[q][e] = i < K ? p.gamma[i] : 0.f;
-      ss = fmaf(x[q][e], x[q][e], ss);
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int i = in ? e0 + 4 * v4 : 0;
+        const float4 u = *reinterpret_cast<const float4 *>(p.a + i);
+        const float4 gv = *reinterpret_cast<const float4 *>(p.gamma + i);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p.mode != kGluePlain) v = *reinterpret_cast<const float4 *>(p.b + i);
+        x[q][4 * v4] = in ? norm_x_of(p.mode, u.x, v.x) : 0.f;
+        x[q][4 * v4 + 1] = in ? norm_x_of(p.mode, u.y, v.y) : 0.f;
+        x[q][4 * v4 + 2] = in ? norm_x_of(p.mode, u.z, v.z) : 0.f;
+        x[q][4 * v4 + 3] = in ? norm_x_of(p.mode, u.w, v.w) : 0.f;
+        g[q][4 * v4] = in ? gv.x : 0.f;
+        g[q][4 * v4 + 1] = in ? gv.y : 0.f;
+        g[q][4 * v4 + 2] = in ? gv.z : 0.f;
+        g[q][4 * v4 + 3] = in ? gv.w : 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int i = e0 + e;
+        x[q][e] = i < K ? norm_x(p, i) : 0.f;
+        g[q][e] = i < K ? p.gamma[i] : 0.f;
+      }
     }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss = fmaf(x[q][e], x[q][e], ss);
   }
   if (p.h_out && b == 0) {
 #pragma unroll
-    for (int q = 0; q < kNormGroupsPerThread; ++q)
+    for (int q = 0; q < kNormGroupsPerThread; ++q) {
+      const int e0 = 16 * (tid + 256 * q);
+      if (VEC) {
+        if (e0 < K)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (16 * (tid + 256 * q) + e < K) p.h_out[16 * (tid + 256 * q) + e] = x[q][e];
+          for (int v4 = 0; v4 < 4; ++v4)
+            *reinterpret_cast<float4 *>(p.h_out + e0 + 4 * v4) =
+                make_float4(x[q][4 * v4], x[q][4 * v4 + 1], x[q][4 * v4 + 2], x[q][4 * v4 + 3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (e0 + e < K) p.h_out[e0 + e] = x[q][e];
+      }
+    }
   }
   // block sum (4 waves); the same tree in every workgroup
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = wave_sum_f(ss);
   if (lane == 0) red[wv_id] = ss;
   __syncthreads();
   const float sum_sq = (red[0] + red[1]) + (red[2] + red[3]);
@@ -270,7 +333,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
       x[q][e] = norm_y(x[q][e], inv, g[q][e]);  // zero past K (x = 0)
       mx = fmaxf(mx, fabsf(x[q][e]));
     }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = wave_max_f(mx);
   __syncthreads();  // everyone has read red[] as sums
   if (lane == 0) red[wv_id] = mx;
   __syncthreads();
