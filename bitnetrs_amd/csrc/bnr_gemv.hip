@@ -184,8 +184,9 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
 // forms x from f32 inputs (a | a + b | max(a,0)^2 * b), reduces sum(x^2) and
 // max|y| with the same tree, and so derives the same int8 activations and
 // the same scale as norm_quant_kernel would; the int8 vector never leaves
-// LDS.  The workgroup issues its weight loads first, so the prologue runs
-// under their latency.  K <= 8192 (one LDS pass); workgroup 0 writes h_out
+// LDS.  The workgroup issues the (cache-resident) activation loads first and
+// its weight loads right after, so the prologue runs under the weights'
+// latency.  K <= 8192 (one LDS pass); workgroup 0 writes h_out
 // (mode residual), which must not alias a or b.
 // ---------------------------------------------------------------------------
 constexpr int kNormK = 8192;
@@ -255,7 +256,32 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
   const int K = a.in_features, nb = (K + 3) / 4;
   const int row = (b - off) * kRowsPerWg + slot;
   const long long b0 = (long long)min(row, m - 1) * a.packed_cols;
-  // 1. this lane's weight pieces (in flight during the prologue)
+  // 1. x for groups tid, tid+256 (16 consecutive elements each) and gamma,
+  // loaded before the weights: loads return in order, so these small,
+  // cache-resident vectors arrive first and the prologue runs while the
+  // weights are still in flight.  VEC: K % 16 == 0 and 16-byte aligned
+  // vectors, so a group is four float4 loads of each input.
+  float x[kNormGroupsPerThread][16], g[kNormGroupsPerThread][16];
+  float4 xa[VEC ? kNormGroupsPerThread : 1][4], xb[VEC ? kNormGroupsPerThread : 1][4],
+      xg[VEC ? kNormGroupsPerThread : 1][4];
+  if (VEC) {
+    // One batch of loads, no branches between them: the second operand is a
+    // itself when the mode has none; groups past K read group 0 (discarded).
+    const float *pb = p.mode == kGluePlain ? p.a : p.b;
+#pragma unroll
+    for (int q = 0; q < kNormGroupsPerThread; ++q) {
+      const int e0 = 16 * (tid + 256 * q);
+      const int base = e0 < K ? e0 : 0;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        xa[q][v4] = *reinterpret_cast<const float4 *>(p.a + base + 4 * v4);
+        xb[q][v4] = *reinterpret_cast<const float4 *>(pb + base + 4 * v4);
+        xg[q][v4] = *reinterpret_cast<const float4 *>(p.gamma + base + 4 * v4);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weights
+  // 2. this lane's weight pieces (in flight during the prologue)
   uint4 wq[kNormPiecesPerLane];
 #pragma unroll
   for (int i = 0; i < kNormPiecesPerLane; ++i) {
@@ -265,23 +291,13 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
     else
       wq[i] = 16 * c < nb ? load16_bounded(w, b0 + 16 * c, b0 + nb) : make_uint4(0, 0, 0, 0);
   }
-  // 2. x for groups tid, tid+256 (16 consecutive elements each), sum of
-  // squares.  VEC: K % 16 == 0 and 16-byte aligned vectors, so a group is
-  // four float4 loads of each input.
-  float x[kNormGroupsPerThread][16], g[kNormGroupsPerThread][16];
-  float ss = 0.f;
+  if (VEC) {
 #pragma unroll
-  for (int q = 0; q < kNormGroupsPerThread; ++q) {
-    const int e0 = 16 * (tid + 256 * q);
-    if (VEC) {
-      const bool in = e0 < K;
+    for (int q = 0; q < kNormGroupsPerThread; ++q) {
+      const bool in = 16 * (tid + 256 * q) < K;
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
-        const int i = in ? e0 + 4 * v4 : 0;
-        const float4 u = *reinterpret_cast<const float4 *>(p.a + i);
-        const float4 gv = *reinterpret_cast<const float4 *>(p.gamma + i);
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (p.mode != kGluePlain) v = *reinterpret_cast<const float4 *>(p.b + i);
+        const float4 u = xa[q][v4], v = xb[q][v4], gv = xg[q][v4];
         x[q][4 * v4] = in ? norm_x_of(p.mode, u.x, v.x) : 0.f;
         x[q][4 * v4 + 1] = in ? norm_x_of(p.mode, u.y, v.y) : 0.f;
         x[q][4 * v4 + 2] = in ? norm_x_of(p.mode, u.z, v.z) : 0.f;
@@ -291,7 +307,11 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
         g[q][4 * v4 + 2] = in ? gv.z : 0.f;
         g[q][4 * v4 + 3] = in ? gv.w : 0.f;
       }
-    } else {
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < kNormGroupsPerThread; ++q) {
+      const int e0 = 16 * (tid + 256 * q);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int i = e0 + e;
@@ -299,9 +319,13 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
         g[q][e] = i < K ? p.gamma[i] : 0.f;
       }
     }
+  }
+  // 3. sum of squares
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < kNormGroupsPerThread; ++q)
 #pragma unroll
     for (int e = 0; e < 16; ++e) ss = fmaf(x[q][e], x[q][e], ss);
-  }
   if (p.h_out && b == 0) {
 #pragma unroll
     for (int q = 0; q < kNormGroupsPerThread; ++q) {
