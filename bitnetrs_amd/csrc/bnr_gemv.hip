@@ -101,6 +101,20 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *w, const int8_t *act, f
     const int kn = min(kPass, in_features - k0);     // activations of this pass
     const long long b0 = prow + k0 / 4;              // first packed byte of the pass
     const int nb = (kn + 3) / 4;                     // packed bytes of the pass
+    // Activation groups first: loads return in order, so the small,
+    // cache-resident activations arrive (and go to LDS) while the weights
+    // are still in flight.
+    uint4 xa[kGroups / 256];
+#pragma unroll
+    for (int t = 0; t < kGroups / 256; ++t) {
+      const int a0 = 16 * (tid + 256 * t);
+      if (VEC && a0 + 16 <= kn) {
+        xa[t] = *reinterpret_cast<const uint4 *>(act + k0 + a0);
+      } else {
+        xa[t] = load16_bounded(reinterpret_cast<const uint8_t *>(act), (long long)k0 + a0,
+                               (long long)k0 + kn);
+      }
+    }
     uint4 wv[kPiecesPerLane];
 #pragma unroll
     for (int i = 0; i < kPiecesPerLane; ++i) {
@@ -112,16 +126,10 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *w, const int8_t *act, f
       }
     }
     __syncthreads();  // the previous pass has finished reading s_act
-    for (int g = tid; g < kGroups; g += 256) {
-      const int a0 = 16 * g;
-      uint4 x;
-      if (VEC && a0 + 16 <= kn) {
-        x = *reinterpret_cast<const uint4 *>(act + k0 + a0);
-      } else {
-        x = load16_bounded(reinterpret_cast<const uint8_t *>(act), (long long)k0 + a0,
-                           (long long)k0 + kn);
-      }
-      s_act[(g & 3) * kPieces + (g >> 2)] = transpose_bytes(x);
+#pragma unroll
+    for (int t = 0; t < kGroups / 256; ++t) {
+      const int g = tid + 256 * t;
+      s_act[(g & 3) * kPieces + (g >> 2)] = transpose_bytes(xa[t]);
     }
     __syncthreads();
 #pragma unroll
