@@ -274,6 +274,49 @@ def test_dev_batched_decode_edge_lengths(backend):
         assert_close(got[b], oracle_decode(w)[4], f"seq {b} len {lens[b]}")
 
 
+@pytest.mark.parametrize("pos", [40000, 70000])
+def test_dev_decode_step_long_context(backend, pos):
+    """Contexts past 256 splits of 128 rows: each split runs several passes
+    over its rows and the last split merges its 150+ partners in rounds of
+    64 (one load round trip each)."""
+    case(f"fused decode step long context pos {pos}")
+    import torch
+
+    cap = pos + 64
+    w = decode_workload(11, pos, cap=cap, q_scale=2.0)
+    q_ref, k_ref, kc_ref, vc_ref, out_ref = oracle_decode(w)
+    kc, vc = dev(w["k_cache"]), dev(w["v_cache"])
+    out = torch.zeros(HQ * D, device="cuda")
+    backend.dev_decode_step(dev(w["q"]), dev(w["k"]), dev(w["v"]), pos, HQ, HKV, D, THETA, kc, vc,
+                            cap, out)
+    np.testing.assert_array_equal(host(kc)[:, pos], kc_ref[:, pos])
+    np.testing.assert_array_equal(host(vc)[:, pos], vc_ref[:, pos])
+    assert_close(host(out), out_ref, f"decode pos {pos}")
+
+
+def test_dev_batched_decode_long_and_short(backend):
+    """A large launch (64-row splits merged by the second kernel) with one
+    sequence long enough for several passes per split and one short one."""
+    case("batched decode lengths 40000 and 100")
+    import torch
+
+    lens = np.array([40000, 100], np.int32)
+    B, cap = len(lens), 40064
+    q = oracle.normal(seed(43, 0), (B, HQ * D))
+    k = oracle.normal(seed(43, 1), (B, HKV * D))
+    v = oracle.normal(seed(43, 2), (B, HKV * D))
+    kc = oracle.normal(seed(43, 3), (B, HKV, cap, D))
+    vc = oracle.normal(seed(43, 4), (B, HKV, cap, D))
+    out = torch.zeros(B, HQ * D, device="cuda")
+    backend.dev_decode_step_batched(dev(q), dev(k), dev(v), lens, HQ, HKV, D, THETA, dev(kc),
+                                    dev(vc), cap, out)
+    got = host(out)
+    for b in range(B):
+        w = {"q": q[b], "k": k[b], "v": v[b], "k_cache": kc[b], "v_cache": vc[b],
+             "pos": int(lens[b]), "cap": cap}
+        assert_close(got[b], oracle_decode(w)[4], f"seq {b} len {lens[b]}")
+
+
 @pytest.mark.parametrize("n_tokens,start", [(2048, 0), (100, 0), (37, 200)])
 def test_dev_prefill(backend, n_tokens, start):
     case(f"prefill n {n_tokens} start {start}")
