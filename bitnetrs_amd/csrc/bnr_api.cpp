@@ -475,8 +475,9 @@ bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
 }
 
 // Split-K plan: rows per 16-lane row group (RPG) and passes so that the grid
-// has about target_wgs workgroups and at most kMaxSplits splits per
-// (sequence, kv head).
+// has about target_wgs workgroups, fits one round of resident workgroups
+// (small launches) and has at most kMaxSplits splits per (sequence, kv
+// head).
 void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeArgs &a) {
   static const int rpgs[4] = {8, 4, 2, 1};
   int rpg = 1;
@@ -487,7 +488,10 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
   // second kernel, so that workgroups never wait on their partial stores.
   // Small launches: the fewest splits that still give about target_wgs
   // workgroups, merged in-kernel by the last workgroup.
-  const bool large = wgs4 >= c->large_wgs;
+  // A single sequence never takes the large path: its parallelism is the
+  // splits, and below it the launch is kept to one round of resident
+  // workgroups instead.
+  const bool large = batch > 1 && wgs4 >= c->large_wgs;
   a.merge_inline = c->merge_mode >= 0 ? c->merge_mode : (large ? 0 : 1);
   if (c->force_rpg) {
     rpg = c->force_rpg;
@@ -505,7 +509,19 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
   }
   int max_chunks = 0;
   for (int b = 0; b < batch; ++b) max_chunks = std::max(max_chunks, (lens[b] + 16 * rpg - 1) / (16 * rpg));
-  const int passes = std::max(1, (max_chunks + kMaxSplits - 1) / kMaxSplits);
+  int passes = std::max(1, (max_chunks + kMaxSplits - 1) / kMaxSplits);
+  if (!large) {
+    // Small launches: more passes per split (each a further load round trip
+    // of the workgroup) rather than a second round of workgroups -- the
+    // RPG-8 kernel holds one workgroup per CU, the others two or three.
+    const long long resident = (long long)c->n_cu * (rpg == 8 ? 1 : rpg == 4 ? 2 : 3);
+    auto wgs_at = [&](int p) {
+      long long w = 0;
+      for (int b = 0; b < batch; ++b) w += (lens[b] + 16 * rpg * p - 1) / (16 * rpg * p);
+      return w * n_kv;
+    };
+    while (wgs_at(passes) > resident && passes < max_chunks) ++passes;
+  }
   const int rows = 16 * rpg * passes;
   a.rpg = rpg;
   a.passes = passes;
