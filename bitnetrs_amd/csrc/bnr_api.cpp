@@ -201,6 +201,7 @@ struct bnr_ctx {
   int target_wgs = 160;
   int large_wgs = 1024;
   int force_rpg = 0;
+  int min_passes = 1;
   int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel
 
   // prefill planner
@@ -509,7 +510,7 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
   }
   int max_chunks = 0;
   for (int b = 0; b < batch; ++b) max_chunks = std::max(max_chunks, (lens[b] + 16 * rpg - 1) / (16 * rpg));
-  int passes = std::max(1, (max_chunks + kMaxSplits - 1) / kMaxSplits);
+  int passes = std::max(c->min_passes, (max_chunks + kMaxSplits - 1) / kMaxSplits);
   if (!large) {
     // Small launches: more passes per split (each a further load round trip
     // of the workgroup) rather than a second round of workgroups -- the
@@ -639,6 +640,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   }
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = atoi(v) != 0;
+  if (const char *v = std::getenv("BNR_DECODE_PASSES")) c->min_passes = std::min(64, std::max(1, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
     if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;

@@ -10,6 +10,8 @@
 // and serves the G query heads of the group from registers (the reference
 // re-reads every row once per query head, bitnet-cpu/src/attention.rs:
 // 170-204).
+#include <type_traits>
+
 #include "bnr_internal.h"
 
 #include <hip/hip_runtime.h>
@@ -469,37 +471,65 @@ void decode_kernel(DecodeArgs a) {
         }
       }
     }
-    float sc[RPG][G];
-#pragma unroll
-    for (int i = 0; i < RPG; ++i) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float d = row_sum16(dot8(qlo[g], qhi[g], klo[i], khi[i]));
-        sc[i][g] = valid[i] ? d : -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float mp = sc[0][g];
-#pragma unroll
-      for (int i = 1; i < RPG; ++i) mp = fmaxf(mp, sc[i][g]);
-      const float m_new = fmaxf(m_run[g], mp);
-      if (m_new == -INFINITY) continue;  // no valid row yet in this row group
-      const float alpha = fast_exp2(m_run[g] - m_new);
-      float lsum = l_run[g] * alpha;
-      float4 alo = scale4(alpha, olo[g]), ahi = scale4(alpha, ohi[g]);
+    // FAST: the first pass with every row of the pass valid (every split of
+    // a context that is a multiple of the split size) -- no row masks and
+    // no rescale of the empty running state.  Only in the in-kernel merge
+    // variants: the second copy of the loop body would make the batched
+    // kernel (three workgroups per CU) spill.
+    auto attend = [&](auto fast) {
+      constexpr bool FAST = decltype(fast)::value;
+      float sc[RPG][G];
 #pragma unroll
       for (int i = 0; i < RPG; ++i) {
-        const float pr = valid[i] ? fast_exp2(sc[i][g] - m_new) : 0.f;
-        lsum += pr;
-        alo = axpy4(pr, vlo[i], alo);
-        ahi = axpy4(pr, vhi[i], ahi);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float d = row_sum16(dot8(qlo[g], qhi[g], klo[i], khi[i]));
+          sc[i][g] = (FAST || valid[i]) ? d : -INFINITY;
+        }
       }
-      m_run[g] = m_new;
-      l_run[g] = lsum;
-      olo[g] = alo;
-      ohi[g] = ahi;
-    }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mp = sc[0][g];
+#pragma unroll
+        for (int i = 1; i < RPG; ++i) mp = fmaxf(mp, sc[i][g]);
+        if (FAST) {
+          float lsum = 0.f;
+          float4 alo, ahi;
+#pragma unroll
+          for (int i = 0; i < RPG; ++i) {
+            const float pr = fast_exp2(sc[i][g] - mp);
+            lsum += pr;
+            alo = i == 0 ? scale4(pr, vlo[0]) : axpy4(pr, vlo[i], alo);
+            ahi = i == 0 ? scale4(pr, vhi[0]) : axpy4(pr, vhi[i], ahi);
+          }
+          m_run[g] = mp;
+          l_run[g] = lsum;
+          olo[g] = alo;
+          ohi[g] = ahi;
+          continue;
+        }
+        const float m_new = fmaxf(m_run[g], mp);
+        if (m_new == -INFINITY) continue;  // no valid row yet in this row group
+        const float alpha = fast_exp2(m_run[g] - m_new);
+        float lsum = l_run[g] * alpha;
+        float4 alo = scale4(alpha, olo[g]), ahi = scale4(alpha, ohi[g]);
+#pragma unroll
+        for (int i = 0; i < RPG; ++i) {
+          const float pr = valid[i] ? fast_exp2(sc[i][g] - m_new) : 0.f;
+          lsum += pr;
+          alo = axpy4(pr, vlo[i], alo);
+          ahi = axpy4(pr, vhi[i], ahi);
+        }
+        m_run[g] = m_new;
+        l_run[g] = lsum;
+        olo[g] = alo;
+        ohi[g] = ahi;
+      }
+    };
+    if (INLINE && p == 0 && tp + 16 * RPG <= t1)
+      attend(std::true_type{});
+    else
+      attend(std::false_type{});
   }
 
   // ---- merge the 16 row-group states through LDS ----
