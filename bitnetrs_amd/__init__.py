@@ -10,9 +10,9 @@ in ``include/bitnet_hip.h``.  ``HipBackend`` mirrors the reference's
 from ._lib import LIB_PATH, build, load
 from .stack import AttentionStack
 from .backend import (BNR_MIRROR_FULL, BNR_MIRROR_INCREMENTAL, BackendError, BitNetError,
-                      DeviceKVCache, HipBackend, InvalidConfig, InvalidShape, QuantizationError,
-                      UnsupportedDevice)
+                      DeviceKVCache, HipBackend, InvalidConfig, InvalidShape, NativeKVCache,
+                      QuantizationError, UnsupportedDevice)
 
-__all__ = ["HipBackend", "DeviceKVCache", "AttentionStack", "BitNetError", "InvalidShape",
+__all__ = ["HipBackend", "DeviceKVCache", "NativeKVCache", "AttentionStack", "BitNetError", "InvalidShape",
            "InvalidConfig", "BackendError", "UnsupportedDevice", "QuantizationError",
            "BNR_MIRROR_FULL", "BNR_MIRROR_INCREMENTAL", "build", "load", "LIB_PATH"]

@@ -127,6 +127,19 @@ SIGNATURES = {
                                                    _vp, _vp, _c.c_float, _vp, _c.POINTER(_vp),
                                                    _c.POINTER(_sz), _sz, _vp]),
     "bnr_dev_synchronize": (_c.c_int, [_vp, _vp]),
+    "bnr_kv_cache_create": (_c.c_int, [_vp, _sz, _sz, _sz, _sz, _c.POINTER(_vp)]),
+    "bnr_kv_cache_destroy": (None, [_vp]),
+    "bnr_kv_cache_clear": (_c.c_int, [_vp]),
+    "bnr_kv_cache_advance": (_c.c_int, [_vp, _sz]),
+    "bnr_kv_cache_len": (_sz, [_vp]),
+    "bnr_kv_cache_layer_len": (_c.c_int, [_vp, _sz, _c.POINTER(_sz)]),
+    "bnr_kv_cache_layer": (_c.c_int, [_vp, _sz, _c.POINTER(_vp), _c.POINTER(_vp)]),
+    "bnr_kv_decode": (_c.c_int, [_vp, _vp, _sz, _f, _sz, _f, _sz, _f, _sz, _sz, _sz, _c.c_float,
+                                 _f, _sz]),
+    "bnr_kv_dev_decode": (_c.c_int, [_vp, _vp, _sz, _vp, _vp, _vp, _sz, _sz, _c.c_float, _vp,
+                                     _vp]),
+    "bnr_kv_dev_prefill": (_c.c_int, [_vp, _vp, _sz, _vp, _vp, _vp, _sz, _sz, _sz, _c.c_float,
+                                      _vp, _vp]),
 }
 
 _lib = None

@@ -21,7 +21,7 @@ from . import _lib
 from ._lib import (BNR_MIRROR_FULL, BNR_MIRROR_INCREMENTAL, BackendError, BitNetError,
                    InvalidConfig, InvalidShape, QuantizationError, UnsupportedDevice)
 
-__all__ = ["HipBackend", "DeviceKVCache", "BitNetError", "InvalidShape", "InvalidConfig",
+__all__ = ["HipBackend", "DeviceKVCache", "NativeKVCache", "BitNetError", "InvalidShape", "InvalidConfig",
            "BackendError", "UnsupportedDevice", "QuantizationError", "BNR_MIRROR_FULL",
            "BNR_MIRROR_INCREMENTAL"]
 
@@ -336,3 +336,74 @@ class DeviceKVCache:
 
     def __len__(self) -> int:
         return self.filled_positions
+
+
+class NativeKVCache:
+    """The library's backend-owned KV cache (``bnr_kv_cache``): KVCache
+    (bitnet-model/src/lib.rs:118-315) with its buffers in HBM, owned and
+    bookkept by libbitnet_hip.so -- what a Rust caller binds.  Rows are
+    written by :meth:`decode` / :meth:`dev_decode` / :meth:`dev_prefill`,
+    which apply store_kv's position rules."""
+
+    def __init__(self, backend: HipBackend, n_layers: int, n_kv_heads: int, head_dim: int,
+                 max_seq: int):
+        self._be = backend
+        self._L = backend._L
+        h = ctypes.c_void_p()
+        _lib.check(self._L.bnr_kv_cache_create(backend._h, n_layers, n_kv_heads, head_dim,
+                                               max_seq, ctypes.byref(h)))
+        self._h = h
+        self.n_layers, self.n_kv_heads, self.head_dim, self.max_seq = (
+            n_layers, n_kv_heads, head_dim, max_seq)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.bnr_kv_cache_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return int(self._L.bnr_kv_cache_len(self._h))
+
+    def advance(self, n: int = 1) -> None:
+        _lib.check(self._L.bnr_kv_cache_advance(self._h, n))
+
+    def clear(self) -> None:
+        _lib.check(self._L.bnr_kv_cache_clear(self._h))
+
+    def layer_len(self, layer: int) -> int:
+        n = ctypes.c_size_t()
+        _lib.check(self._L.bnr_kv_cache_layer_len(self._h, layer, ctypes.byref(n)))
+        return n.value
+
+    def layer_ptrs(self, layer: int):
+        """Device addresses (K, V) of a layer's ``[n_kv, max_seq, head_dim]`` caches."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(self._L.bnr_kv_cache_layer(self._h, layer, ctypes.byref(k), ctypes.byref(v)))
+        return k.value, v.value
+
+    def decode(self, layer: int, q: np.ndarray, k: np.ndarray, v: np.ndarray, position: int,
+               n_heads: int, theta: float, output: np.ndarray) -> None:
+        """rope_embed -> store_kv -> masked_attention for one token of one layer
+        from host slices; q and k are rotated in place."""
+        _lib.check(self._L.bnr_kv_decode(
+            self._be._h, self._h, layer, _host(q, "q"), q.size, _host(k, "k"), k.size,
+            _host(v, "v"), v.size, position, n_heads, theta, _host(output, "output"),
+            output.size))
+
+    def dev_decode(self, layer: int, q, k, v, position: int, n_heads: int, theta: float, out,
+                   stream=None) -> None:
+        _lib.check(self._L.bnr_kv_dev_decode(
+            self._be._h, self._h, layer, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), position,
+            n_heads, theta, _dev(out, "out"), _stream(stream)))
+
+    def dev_prefill(self, layer: int, q, k, v, n_tokens: int, start_pos: int, n_heads: int,
+                    theta: float, out, stream=None) -> None:
+        _lib.check(self._L.bnr_kv_dev_prefill(
+            self._be._h, self._h, layer, _dev(q, "q"), _dev(k, "k"), _dev(v, "v"), n_tokens,
+            start_pos, n_heads, theta, _dev(out, "out"), _stream(stream)))

@@ -15,6 +15,7 @@
 #include <cstring>
 #include <list>
 #include <mutex>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -1085,22 +1086,16 @@ extern "C" int bnr_dev_decode_attention(bnr_ctx *c, const float *q, const float 
   return st ? st : set_ok();
 }
 
-extern "C" int bnr_dev_decode_step(bnr_ctx *c, const float *q, const float *k, const float *v,
-                                   size_t position, size_t n_heads, size_t n_kv_heads,
-                                   size_t head_dim, float theta, float *k_cache, float *v_cache,
-                                   size_t cap, float *out, float *q_rot, float *k_rot,
-                                   void *stream) {
-  if (!c) return err_backend("context is NULL");
-  int st = check_heads(n_heads, n_kv_heads, head_dim);
-  if (!st) st = check_rope(head_dim, theta);
-  if (!st) st = check_rows(position, cap);
-  if (st) return st;
-  if (!q || !k || !v || !k_cache || !v_cache || !out) return err_backend("decode_step: NULL pointer");
-  std::lock_guard<std::mutex> lk(c->mu);
+namespace {
+
+// bnr_dev_decode_step after validation; the caller holds c->mu.
+int decode_step_locked(bnr_ctx *c, const float *q, const float *k, const float *v,
+                       size_t position, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                       float theta, float *k_cache, float *v_cache, size_t cap, float *out,
+                       float *q_rot, float *k_rot, hipStream_t s) {
   DeviceGuard dg(c->device);
-  st = ensure_table(c, position, head_dim, theta);
+  int st = ensure_table(c, position, head_dim, theta);
   if (st) return st;
-  hipStream_t s = (hipStream_t)stream;
   const long long kv_stride = (long long)(cap * head_dim);
   const bool al = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
                   aligned16(v_cache) && (!q_rot || aligned16(q_rot)) && (!k_rot || aligned16(k_rot));
@@ -1135,6 +1130,24 @@ extern "C" int bnr_dev_decode_step(bnr_ctx *c, const float *q, const float *k, c
   if (!st) st = run_generic(c, qw, k_cache, v_cache, kv_stride, out, n_heads, n_kv_heads, head_dim,
                             position, s);
   return st ? st : set_ok();
+}
+
+}  // namespace
+
+extern "C" int bnr_dev_decode_step(bnr_ctx *c, const float *q, const float *k, const float *v,
+                                   size_t position, size_t n_heads, size_t n_kv_heads,
+                                   size_t head_dim, float theta, float *k_cache, float *v_cache,
+                                   size_t cap, float *out, float *q_rot, float *k_rot,
+                                   void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rope(head_dim, theta);
+  if (!st) st = check_rows(position, cap);
+  if (st) return st;
+  if (!q || !k || !v || !k_cache || !v_cache || !out) return err_backend("decode_step: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  return decode_step_locked(c, q, k, v, position, n_heads, n_kv_heads, head_dim, theta, k_cache,
+                            v_cache, cap, out, q_rot, k_rot, (hipStream_t)stream);
 }
 
 extern "C" int bnr_dev_decode_step_batched(bnr_ctx *c, const float *q, const float *k,
@@ -1672,5 +1685,243 @@ extern "C" int bnr_dev_synchronize(bnr_ctx *c, void *stream) {
   if (!c) return err_backend("context is NULL");
   DeviceGuard dg(c->device);
   HIP_TRY(hipStreamSynchronize((hipStream_t)stream), "synchronize");
+  return set_ok();
+}
+
+// ---------------------------------------------------------------------------
+// Backend-owned KV cache: KVCache (bitnet-model/src/lib.rs:118-315) with its
+// buffers in HBM.  One allocation holds, per layer, K then V, each
+// head-major [n_kv_heads x max_seq x head_dim].  The bookkeeping
+// (layer_lengths, filled_positions) and store_kv's position rules are the
+// reference's; the row itself is written by the decode / prefill kernels.
+// ---------------------------------------------------------------------------
+struct bnr_kv_cache {
+  int device = 0;
+  size_t n_layers = 0, n_kv = 0, head_dim = 0, max_seq = 0;
+  size_t layer_floats = 0;  // n_kv * max_seq * head_dim (one of K or V)
+  float *base = nullptr;
+  std::vector<size_t> layer_len;
+  size_t filled = 0;
+  std::mutex mu;
+
+  float *k(size_t layer) const { return base + 2 * layer * layer_floats; }
+  float *v(size_t layer) const { return base + (2 * layer + 1) * layer_floats; }
+};
+
+namespace {
+
+int kv_check_layer(const bnr_kv_cache *kc, size_t layer) {
+  if (layer >= kc->n_layers)
+    return err_shape(fmt("layer < num_hidden_layers (%zu)", kc->n_layers), fmt("layer = %zu", layer));
+  return BNR_OK;
+}
+
+// store_kv's position rules (lib.rs:204-216) for rows position..position+n-1
+// written in order: each row either overwrites a stored one or extends the
+// layer by one.
+int kv_check_store(const bnr_kv_cache *kc, size_t layer, size_t position, size_t n) {
+  int st = kv_check_layer(kc, layer);
+  if (st) return st;
+  const size_t last = position + n - 1;
+  if (last >= kc->max_seq)
+    return err_shape(fmt("position < max_seq (%zu)", kc->max_seq), fmt("position = %zu", last));
+  if (position > kc->layer_len[layer])
+    return err_shape(fmt("position <= layer_len_positions (%zu)", kc->layer_len[layer]),
+                     fmt("position = %zu", position));
+  return BNR_OK;
+}
+
+void kv_mark_stored(bnr_kv_cache *kc, size_t layer, size_t position, size_t n) {
+  kc->layer_len[layer] = std::max(kc->layer_len[layer], position + n);
+}
+
+size_t round4(size_t n) { return (n + 3) & ~(size_t)3; }
+
+}  // namespace
+
+extern "C" int bnr_kv_cache_create(bnr_ctx *c, size_t n_layers, size_t n_kv_heads, size_t head_dim,
+                                   size_t max_seq, bnr_kv_cache **out) {
+  if (!out) return err_backend("kv_cache_create: NULL out");
+  *out = nullptr;
+  if (!c) return err_backend("context is NULL");
+  if (n_layers == 0) return err_config("num_hidden_layers must be > 0");
+  if (n_kv_heads == 0) return err_config("n_kv_heads must be > 0");
+  if (head_dim == 0) return err_shape("head_dim > 0", "head_dim = 0");
+  if (max_seq == 0) return err_shape("max_seq > 0", "max_seq = 0");
+  const size_t per = n_kv_heads * max_seq * head_dim;
+  if (per / n_kv_heads / head_dim != max_seq || per > SIZE_MAX / 8 / n_layers)
+    return err_shape("a cache size that fits in memory", "an overflowing size");
+  const size_t bytes = 2 * n_layers * per * sizeof(float);
+  DeviceGuard dg(c->device);
+  auto *kc = new (std::nothrow) bnr_kv_cache();
+  if (!kc) return err_backend("kv cache: out of host memory");
+  kc->device = c->device;
+  kc->n_layers = n_layers;
+  kc->n_kv = n_kv_heads;
+  kc->head_dim = head_dim;
+  kc->max_seq = max_seq;
+  kc->layer_floats = per;
+  kc->layer_len.assign(n_layers, 0);
+  hipError_t e = hipMalloc((void **)&kc->base, bytes);
+  if (e == hipSuccess) e = hipMemset(kc->base, 0, bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    if (kc->base) (void)hipFree(kc->base);
+    delete kc;
+    return err_hip(e, "kv cache alloc");
+  }
+  *out = kc;
+  return set_ok();
+}
+
+extern "C" void bnr_kv_cache_destroy(bnr_kv_cache *kc) {
+  if (!kc) return;
+  DeviceGuard dg(kc->device);
+  (void)hipDeviceSynchronize();  // kernels in flight may still use the cache
+  (void)hipFree(kc->base);
+  delete kc;
+}
+
+extern "C" int bnr_kv_cache_clear(bnr_kv_cache *kc) {
+  if (!kc) return err_backend("kv cache is NULL");
+  std::lock_guard<std::mutex> lk(kc->mu);
+  DeviceGuard dg(kc->device);
+  HIP_TRY(hipDeviceSynchronize(), "kv cache clear");
+  HIP_TRY(hipMemset(kc->base, 0, 2 * kc->n_layers * kc->layer_floats * sizeof(float)),
+          "kv cache clear");
+  HIP_TRY(hipDeviceSynchronize(), "kv cache clear");
+  std::fill(kc->layer_len.begin(), kc->layer_len.end(), (size_t)0);
+  kc->filled = 0;
+  return set_ok();
+}
+
+extern "C" int bnr_kv_cache_advance(bnr_kv_cache *kc, size_t n) {
+  if (!kc) return err_backend("kv cache is NULL");
+  std::lock_guard<std::mutex> lk(kc->mu);
+  // KVCache::advance asserts filled_positions < max_seq before each step
+  // (and panics); here nothing advances and the message is an error.
+  if (n > kc->max_seq - kc->filled)
+    return err_backend(fmt("KVCache::advance overflow: filled_positions=%zu max_seq=%zu",
+                           kc->filled, kc->max_seq));
+  kc->filled += n;
+  return set_ok();
+}
+
+extern "C" size_t bnr_kv_cache_len(const bnr_kv_cache *kc) { return kc ? kc->filled : 0; }
+
+extern "C" int bnr_kv_cache_layer_len(bnr_kv_cache *kc, size_t layer, size_t *len) {
+  if (!kc || !len) return err_backend("kv_cache_layer_len: NULL pointer");
+  std::lock_guard<std::mutex> lk(kc->mu);
+  int st = kv_check_layer(kc, layer);
+  if (st) return st;
+  *len = kc->layer_len[layer];
+  return set_ok();
+}
+
+extern "C" int bnr_kv_cache_layer(bnr_kv_cache *kc, size_t layer, float **k, float **v) {
+  if (!kc || !k || !v) return err_backend("kv_cache_layer: NULL pointer");
+  int st = kv_check_layer(kc, layer);
+  if (st) return st;
+  *k = kc->k(layer);
+  *v = kc->v(layer);
+  return set_ok();
+}
+
+extern "C" int bnr_kv_decode(bnr_ctx *c, bnr_kv_cache *kc, size_t layer, float *q, size_t q_len,
+                             float *k, size_t k_len, const float *v, size_t v_len,
+                             size_t position, size_t n_heads, float theta, float *output,
+                             size_t out_len) {
+  if (!c) return err_backend("context is NULL");
+  if (!kc) return err_backend("kv cache is NULL");
+  const size_t hd = kc->head_dim, nkv = kc->n_kv, kvn = nkv * hd;
+  // rope_embed first (RopeCache::new, then apply_rope_cached's lengths:
+  // bitnet-cpu/src/rope.rs:101-110, 324-337) ...
+  int st = check_rope(hd, theta);
+  if (st) return st;
+  if (q_len != n_heads * hd)
+    return err_shape(fmt("q.len() == %zu * %zu = %zu", n_heads, hd, n_heads * hd),
+                     fmt("q.len() = %zu", q_len));
+  if (k_len != kvn)
+    return err_shape(fmt("k.len() == %zu * %zu = %zu", nkv, hd, kvn), fmt("k.len() = %zu", k_len));
+  // ... then store_kv (bitnet-model/src/lib.rs:190-216) ...
+  if (v_len != kvn) return err_shape(fmt("v_vec.len() = %zu", kvn), fmt("%zu", v_len));
+  std::lock_guard<std::mutex> lk(kc->mu);
+  st = kv_check_store(kc, layer, position, 1);
+  if (st) return st;
+  // ... then masked_attention (bitnet-cpu/src/attention.rs:109-161).
+  st = check_heads(n_heads, nkv, hd);
+  if (st) return st;
+  if (out_len != n_heads * hd)
+    return err_shape(fmt("output.len() == n_heads * head_dim = %zu", n_heads * hd),
+                     fmt("output.len() = %zu", out_len));
+  if (!q || !k || !v || !output) return err_backend("kv_decode: NULL slice");
+  if (kc->device != c->device) return err_backend("kv cache and context are on different devices");
+  std::lock_guard<std::mutex> lc(c->mu);
+  DeviceGuard dg(c->device);
+  // Staging: q, k, v in; rotated q, rotated k and the output back.
+  const size_t qs = round4(q_len), ks = round4(kvn);
+  st = ensure_buf(&c->d_q, &c->d_q_n, 2 * qs + 3 * ks, "staging alloc");
+  if (st) return st;
+  st = ensure_buf(&c->d_out, &c->d_out_n, out_len, "staging alloc");
+  if (st) return st;
+  float *dq = c->d_q, *dk = dq + qs, *dv = dk + ks, *dqr = dv + ks, *dkr = dqr + qs;
+  HIP_TRY(hipMemcpyAsync(dq, q, q_len * 4, hipMemcpyHostToDevice, c->stream), "upload q");
+  HIP_TRY(hipMemcpyAsync(dk, k, kvn * 4, hipMemcpyHostToDevice, c->stream), "upload k");
+  HIP_TRY(hipMemcpyAsync(dv, v, kvn * 4, hipMemcpyHostToDevice, c->stream), "upload v");
+  st = decode_step_locked(c, dq, dk, dv, position, n_heads, nkv, hd, theta, kc->k(layer),
+                          kc->v(layer), kc->max_seq, c->d_out, dqr, dkr, c->stream);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(output, c->d_out, out_len * 4, hipMemcpyDeviceToHost, c->stream),
+          "download out");
+  HIP_TRY(hipMemcpyAsync(q, dqr, q_len * 4, hipMemcpyDeviceToHost, c->stream), "download q");
+  HIP_TRY(hipMemcpyAsync(k, dkr, kvn * 4, hipMemcpyDeviceToHost, c->stream), "download k");
+  HIP_TRY(hipStreamSynchronize(c->stream), "kv_decode");
+  kv_mark_stored(kc, layer, position, 1);
+  return set_ok();
+}
+
+extern "C" int bnr_kv_dev_decode(bnr_ctx *c, bnr_kv_cache *kc, size_t layer, const float *q,
+                                 const float *k, const float *v, size_t position, size_t n_heads,
+                                 float theta, float *out, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (!kc) return err_backend("kv cache is NULL");
+  const size_t hd = kc->head_dim, nkv = kc->n_kv;
+  int st = check_rope(hd, theta);
+  if (st) return st;
+  std::lock_guard<std::mutex> lk(kc->mu);
+  st = kv_check_store(kc, layer, position, 1);
+  if (!st) st = check_heads(n_heads, nkv, hd);
+  if (st) return st;
+  if (!q || !k || !v || !out) return err_backend("kv_dev_decode: NULL pointer");
+  if (kc->device != c->device) return err_backend("kv cache and context are on different devices");
+  {
+    std::lock_guard<std::mutex> lc(c->mu);
+    st = decode_step_locked(c, q, k, v, position, n_heads, nkv, hd, theta, kc->k(layer),
+                            kc->v(layer), kc->max_seq, out, nullptr, nullptr, (hipStream_t)stream);
+  }
+  if (st) return st;
+  kv_mark_stored(kc, layer, position, 1);
+  return set_ok();
+}
+
+extern "C" int bnr_kv_dev_prefill(bnr_ctx *c, bnr_kv_cache *kc, size_t layer, float *q, float *k,
+                                  const float *v, size_t n_tokens, size_t start_pos,
+                                  size_t n_heads, float theta, float *out, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if (!kc) return err_backend("kv cache is NULL");
+  int st = check_rope(kc->head_dim, theta);
+  if (st) return st;
+  std::lock_guard<std::mutex> lk(kc->mu);
+  if (n_tokens == 0) {
+    st = kv_check_layer(kc, layer);
+    return st ? st : set_ok();
+  }
+  st = kv_check_store(kc, layer, start_pos, n_tokens);
+  if (st) return st;
+  if (kc->device != c->device) return err_backend("kv cache and context are on different devices");
+  st = bnr_dev_prefill(c, q, k, v, n_tokens, start_pos, n_heads, kc->n_kv, kc->head_dim, theta,
+                       kc->k(layer), kc->v(layer), kc->max_seq, out, stream);
+  if (st) return st;
+  kv_mark_stored(kc, layer, start_pos, n_tokens);
   return set_ok();
 }

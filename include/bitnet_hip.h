@@ -296,6 +296,59 @@ int bnr_dev_ternary_gemv_norm_group(bnr_ctx *ctx, size_t n, const uint8_t *const
 /* Wait for all work the context enqueued on `stream`. */
 int bnr_dev_synchronize(bnr_ctx *ctx, void *stream);
 
+/* ---- Backend-owned KV cache ----------------------------------------------
+ * KVCache (bitnet-model/src/lib.rs:118-315) with its buffers in HBM: per
+ * layer a K and a V cache, each head-major [n_kv_heads x max_seq x head_dim]
+ * fp32, plus the reference's bookkeeping (layer_lengths, filled_positions).
+ * Rows are written only by the decode / prefill calls below, which apply
+ * store_kv's position rules (lib.rs:204-216): a row either overwrites a
+ * stored one or extends its layer by one; position >= max_seq and gaps are
+ * BNR_INVALID_SHAPE with the reference's messages.  Calls on one cache are
+ * serialised by the cache. */
+typedef struct bnr_kv_cache bnr_kv_cache;
+
+/* KVCache::new (lib.rs:148-169): zero-filled caches on the context's device. */
+int bnr_kv_cache_create(bnr_ctx *ctx, size_t n_layers, size_t n_kv_heads, size_t head_dim,
+                        size_t max_seq, bnr_kv_cache **out);
+/* Free the cache's HBM (waits for work in flight on the device). */
+void bnr_kv_cache_destroy(bnr_kv_cache *cache);
+/* KVCache::clear (lib.rs:285-292): zero every layer, reset lengths and
+ * filled_positions.  Waits for all work on the device first. */
+int bnr_kv_cache_clear(bnr_kv_cache *cache);
+/* KVCache::advance (lib.rs:244-252) by n positions.  Where the reference
+ * panics (advancing past max_seq) this returns BNR_BACKEND_ERROR with the
+ * panic's message and advances nothing. */
+int bnr_kv_cache_advance(bnr_kv_cache *cache, size_t n);
+/* KVCache::len (filled_positions, lib.rs:294-298). */
+size_t bnr_kv_cache_len(const bnr_kv_cache *cache);
+/* Positions stored in `layer` (layer_lengths[layer]). */
+int bnr_kv_cache_layer_len(bnr_kv_cache *cache, size_t layer, size_t *len);
+/* Device addresses of layer's K and V caches, for the bnr_dev_* calls with
+ * cap = max_seq (the k_slice / v_slice backing buffers, lib.rs:262-280). */
+int bnr_kv_cache_layer(bnr_kv_cache *cache, size_t layer, float **k, float **v);
+
+/* One token of one layer from host slices: the per-layer sequence of
+ * BitNetModel::forward_into (lib.rs:1004-1036) -- rope_embed(q, k,
+ * position), store_kv(layer, position, k, v), masked_attention(q, layer's
+ * caches, output, cur_pos = position) -- as one kernel launch.  q
+ * [n_heads*head_dim] and k [n_kv_heads*head_dim] are rotated in place as
+ * rope_embed does; v [n_kv_heads*head_dim]; output [n_heads*head_dim].
+ * Validation in the reference's order (rope, store_kv, attention).
+ * Synchronous. */
+int bnr_kv_decode(bnr_ctx *ctx, bnr_kv_cache *cache, size_t layer, float *q, size_t q_len,
+                  float *k, size_t k_len, const float *v, size_t v_len, size_t position,
+                  size_t n_heads, float theta, float *output, size_t out_len);
+/* bnr_kv_decode on device pointers (q, k, v are read, not rotated in
+ * place), ordered on `stream`: bnr_dev_decode_step on the layer's caches. */
+int bnr_kv_dev_decode(bnr_ctx *ctx, bnr_kv_cache *cache, size_t layer, const float *q,
+                      const float *k, const float *v, size_t position, size_t n_heads,
+                      float theta, float *out, void *stream);
+/* bnr_dev_prefill on the layer's caches: n_tokens rows from start_pos
+ * (store_kv's rules for each row in order); q and k rotated in place. */
+int bnr_kv_dev_prefill(bnr_ctx *ctx, bnr_kv_cache *cache, size_t layer, float *q, float *k,
+                       const float *v, size_t n_tokens, size_t start_pos, size_t n_heads,
+                       float theta, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
