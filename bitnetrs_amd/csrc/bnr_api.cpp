@@ -199,7 +199,7 @@ struct bnr_ctx {
   int mirror_mode = BNR_MIRROR_INCREMENTAL;
 
   // decode planner
-  int target_wgs = 160;
+  int target_wgs = 256;  // small decode launches: at most this many workgroups (the CU count)
   int large_wgs = 1024;
   int force_rpg = 0;
   int min_passes = 1;
@@ -476,53 +476,79 @@ bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
   return g == 1 || g == 2 || g == 4;
 }
 
-// Split-K plan: rows per 16-lane row group (RPG) and passes so that the grid
-// has about target_wgs workgroups, fits one round of resident workgroups
-// (small launches) and has at most kMaxSplits splits per (sequence, kv
-// head).
+// Split-K plan: rows per 16-lane row group (RPG) and passes per split.
+// Small launches fit one workgroup per CU and have at most kMaxSplits
+// splits per (sequence, kv head).
 void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeArgs &a) {
-  static const int rpgs[4] = {8, 4, 2, 1};
   int rpg = 1;
   long long wgs4 = 0;  // workgroups at 64 rows each
   for (int b = 0; b < batch; ++b) wgs4 += (lens[b] + 63) / 64;
   wgs4 *= n_kv;
   // Large launches (several workgroups per CU): 64-row splits, merged by a
   // second kernel, so that workgroups never wait on their partial stores.
-  // Small launches: the fewest splits that still give about target_wgs
-  // workgroups, merged in-kernel by the last workgroup.
-  // A single sequence never takes the large path: its parallelism is the
-  // splits, and below it the launch is kept to one round of resident
-  // workgroups instead.
+  // Small launches: merged in-kernel by the last workgroup.  A single
+  // sequence never takes the large path: its parallelism is the splits.
   const bool large = batch > 1 && wgs4 >= c->large_wgs;
   a.merge_inline = c->merge_mode >= 0 ? c->merge_mode : (large ? 0 : 1);
-  if (c->force_rpg) {
-    rpg = c->force_rpg;
-  } else if (large) {
-    rpg = 4;
-  } else {
-    for (int r : rpgs) {
-      long long wgs = 0;
-      for (int b = 0; b < batch; ++b) wgs += (lens[b] + 16 * r - 1) / (16 * r);
-      if (wgs * n_kv >= c->target_wgs) {
-        rpg = r;
-        break;
+  int passes = 1;
+  if (!large && !c->force_rpg) {
+    // Small launches: among the splits of 16 * rpg * passes rows (rpg 1..8)
+    // whose workgroups fit one per CU (at most target_wgs, by default the
+    // CU count), the one with the lowest estimated time
+    //   0.035 us per row of a workgroup + 0.061 us per split merged
+    //   + 0.47 us per pass beyond the first,
+    // a fit to graph-timed single-sequence launches on MI355X (contexts
+    // 512-8192, rpg 1-8): rows cost the workgroup's loads and arithmetic,
+    // splits cost the merge's loads, and each extra pass a load round trip.
+    long long best = -1;
+    rpg = 8;
+    passes = 1;
+    int max_len = 1;
+    for (int b = 0; b < batch; ++b) max_len = std::max(max_len, lens[b]);
+    const int p_max = std::max(c->min_passes, (max_len + 15) / 16);
+    for (int p = c->min_passes; p <= p_max; ++p) {
+      // No split of p passes beats `best` once its least cost (rpg 1, one
+      // split) does not.
+      if (best >= 0 && 35LL * 16 * p + 61LL + 474LL * (p - 1) >= best) break;
+      for (int r = 1; r <= 8; ++r) {
+        if (!a.merge_inline && (r & (r - 1))) continue;  // two-launch kernels: rpg 1, 2, 4, 8
+        const int rows = 16 * r * p;
+        long long wgs = 0;
+        int splits = 0;
+        for (int b = 0; b < batch; ++b) {
+          const int ns = (lens[b] + rows - 1) / rows;
+          wgs += ns;
+          splits = std::max(splits, ns);
+        }
+        if (wgs * n_kv > c->target_wgs) continue;
+        const long long cost = 35LL * rows + 61LL * splits + 474LL * (p - 1);
+        if (best < 0 || cost < best) {
+          best = cost;
+          rpg = r;
+          passes = p;
+        }
       }
     }
-  }
-  int max_chunks = 0;
-  for (int b = 0; b < batch; ++b) max_chunks = std::max(max_chunks, (lens[b] + 16 * rpg - 1) / (16 * rpg));
-  int passes = std::max(c->min_passes, (max_chunks + kMaxSplits - 1) / kMaxSplits);
-  if (!large) {
-    // Small launches: more passes per split (each a further load round trip
-    // of the workgroup) rather than a second round of workgroups -- the
-    // RPG-8 kernel holds one workgroup per CU, the others two or three.
-    const long long resident = (long long)c->n_cu * (rpg == 8 ? 1 : rpg == 4 ? 2 : 3);
-    auto wgs_at = [&](int p) {
-      long long w = 0;
-      for (int b = 0; b < batch; ++b) w += (lens[b] + 16 * rpg * p - 1) / (16 * rpg * p);
-      return w * n_kv;
-    };
-    while (wgs_at(passes) > resident && passes < max_chunks) ++passes;
+    if (best < 0)  // more (sequence, kv head) pairs than target_wgs: one split each
+      passes = std::max(c->min_passes, (max_len + 16 * 8 - 1) / (16 * 8));
+  } else {
+    rpg = c->force_rpg ? c->force_rpg : 4;
+    if (!a.merge_inline && (rpg & (rpg - 1))) rpg = 4;  // two-launch kernels: rpg 1, 2, 4, 8
+    int max_chunks = 0;
+    for (int b = 0; b < batch; ++b) max_chunks = std::max(max_chunks, (lens[b] + 16 * rpg - 1) / (16 * rpg));
+    passes = std::max(c->min_passes, (max_chunks + kMaxSplits - 1) / kMaxSplits);
+    if (!large) {
+      // A forced rpg: more passes per split rather than a second round of
+      // workgroups (the RPG-6/8 kernels hold one workgroup per CU, the
+      // others two or three).
+      const long long resident = (long long)c->n_cu * (rpg >= 5 ? 1 : rpg >= 3 ? 2 : 3);
+      auto wgs_at = [&](int p) {
+        long long w = 0;
+        for (int b = 0; b < batch; ++b) w += (lens[b] + 16 * rpg * p - 1) / (16 * rpg * p);
+        return w * n_kv;
+      };
+      while (wgs_at(passes) > resident && passes < max_chunks) ++passes;
+    }
   }
   const int rows = 16 * rpg * passes;
   a.rpg = rpg;
@@ -639,14 +665,15 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     delete c;
     return err_hip(e, "hipStreamCreate");
   }
+  if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
+  c->target_wgs = c->n_cu;
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = atoi(v) != 0;
   if (const char *v = std::getenv("BNR_DECODE_PASSES")) c->min_passes = std::min(64, std::max(1, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
-    if (r == 1 || r == 2 || r == 4 || r == 8) c->force_rpg = r;
+    if (r >= 1 && r <= 8) c->force_rpg = r;
   }
-  if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
   if (const char *v = std::getenv("BNR_PREFILL_CHUNK_SHIFT")) c->pf_chunk_shift = std::min(std::max(atoi(v), 0), 20);
   if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT")) c->pf_persistent = atoi(v) > 0;
   *out = c;

@@ -1125,12 +1125,25 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeGenericArgs a
 template <int G, bool INLINE, bool RAGGED>
 hipError_t launch_decode_gir(const DecodeArgs &a, hipStream_t s) {
   dim3 grid(a.max_splits, a.n_kv, a.batch), block(256);
+  // Every rpg 1..8 for the in-kernel merge (small launches); 1, 2, 4, 8 for
+  // the two-launch merge (large launches use 4).
   switch (a.rpg) {
     case 1: decode_kernel<G, 1, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
     case 2: decode_kernel<G, 2, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
     case 4: decode_kernel<G, 4, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
     case 8: decode_kernel<G, 8, INLINE, RAGGED><<<grid, block, 0, s>>>(a); break;
-    default: return hipErrorInvalidValue;
+    default:
+      if constexpr (INLINE) {
+        switch (a.rpg) {
+          case 3: decode_kernel<G, 3, true, RAGGED><<<grid, block, 0, s>>>(a); break;
+          case 5: decode_kernel<G, 5, true, RAGGED><<<grid, block, 0, s>>>(a); break;
+          case 6: decode_kernel<G, 6, true, RAGGED><<<grid, block, 0, s>>>(a); break;
+          case 7: decode_kernel<G, 7, true, RAGGED><<<grid, block, 0, s>>>(a); break;
+          default: return hipErrorInvalidValue;
+        }
+      } else {
+        return hipErrorInvalidValue;
+      }
   }
   if (!INLINE && a.max_splits > 1)
     decode_merge_kernel<G><<<dim3(a.n_kv * G, a.batch), block, 0, s>>>(a);

@@ -55,12 +55,13 @@ def decode_step(be, w, n_heads=HQ, n_kv=HKV, hd=D):
     return host(out), host(kc)
 
 
-@pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("rpg", [1, 2, 8])
+@pytest.mark.parametrize("mode,rpg", [(0, 1), (0, 2), (0, 8), (1, 1), (1, 2), (1, 3), (1, 5),
+                                      (1, 6), (1, 7), (1, 8), (1, None)])
 def test_decode_merge_modes_consecutive(monkeypatch, mode, rpg):
     """Positions 300, 900, 2000, 64, 4095 in a row.  With 16*rpg rows per
     split these give 1..128 splits per kv head: merge rounds of 16, 32, 48
-    and 64 splits, and two rounds above 64."""
+    and 64 splits, and two rounds above 64.  rpg None: the planner's
+    choice (the smallest split that fits one workgroup per CU)."""
     be = fresh_backend(monkeypatch, mode, rpg)
     try:
         for i, pos in enumerate((300, 900, 2000, 64, 4095)):
