@@ -1729,7 +1729,7 @@ struct bnr_kv_cache {
   float *base = nullptr;
   std::vector<size_t> layer_len;
   size_t filled = 0;
-  std::mutex mu;
+  mutable std::mutex mu;  // bookkeeping; calls on one cache are serialised
 
   float *k(size_t layer) const { return base + 2 * layer * layer_floats; }
   float *v(size_t layer) const { return base + (2 * layer + 1) * layer_floats; }
@@ -1834,7 +1834,11 @@ extern "C" int bnr_kv_cache_advance(bnr_kv_cache *kc, size_t n) {
   return set_ok();
 }
 
-extern "C" size_t bnr_kv_cache_len(const bnr_kv_cache *kc) { return kc ? kc->filled : 0; }
+extern "C" size_t bnr_kv_cache_len(const bnr_kv_cache *kc) {
+  if (!kc) return 0;
+  std::lock_guard<std::mutex> lk(kc->mu);
+  return kc->filled;
+}
 
 extern "C" int bnr_kv_cache_layer_len(bnr_kv_cache *kc, size_t layer, size_t *len) {
   if (!kc || !len) return err_backend("kv_cache_layer_len: NULL pointer");
