@@ -479,7 +479,11 @@ bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
 // Split-K plan: rows per 16-lane row group (RPG) and passes per split.
 // Small launches fit one workgroup per CU and have at most kMaxSplits
 // splits per (sequence, kv head).
-void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeArgs &a) {
+}  // namespace
+
+void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, int n_kv,
+                      DecodeArgs &a) {
+  const DecodePlanConfig *c = &cfg;
   int rpg = 1;
   long long wgs4 = 0;  // workgroups at 64 rows each
   for (int b = 0; b < batch; ++b) wgs4 += (lens[b] + 63) / 64;
@@ -564,6 +568,8 @@ void plan_decode(const bnr_ctx *c, const int *lens, int batch, int n_kv, DecodeA
   }
 }
 
+namespace {
+
 // Launch the fast decode kernel over `batch` (<= kMaxBatchPerLaunch)
 // sequences; a.{q,k_new,...,strides} are filled by the caller.
 int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n_kv, int group,
@@ -573,7 +579,9 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
     lens[b] = positions[b] + 1;
     a.positions[b] = positions[b];
   }
-  plan_decode(c, lens, batch, n_kv, a);
+  const DecodePlanConfig pc{c->n_cu, c->target_wgs, c->large_wgs, c->force_rpg, c->min_passes,
+                            c->merge_mode};
+  plan_decode(pc, lens, batch, n_kv, a);
   a.n_kv = n_kv;
   a.group = group;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);

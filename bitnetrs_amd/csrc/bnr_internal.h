@@ -61,6 +61,20 @@ struct DecodeArgs {
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 
+// Decode planner inputs: the device and the context's tuning state.
+struct DecodePlanConfig {
+  int n_cu;        // CUs of the device
+  int target_wgs;  // small launches: at most this many workgroups (default n_cu)
+  int large_wgs;   // launches of at least this many 64-row workgroups use the two-launch merge
+  int force_rpg;   // 0, or a fixed rows-per-row-group (tuning)
+  int min_passes;  // at least this many passes per split (tuning, default 1)
+  int merge_mode;  // -1: planner decides; 0: second kernel; 1: in-kernel
+};
+// Split-K plan of one decode launch over sequences of lens[b] rows: fills
+// a.rpg, a.passes, a.rows_per_split, a.batch, a.split_off, a.max_splits and
+// a.merge_inline.
+void plan_decode(const DecodePlanConfig &c, const int *lens, int batch, int n_kv, DecodeArgs &a);
+
 // Any head_dim / group size: one workgroup per query head, scores staged in
 // a global workspace [n_heads][L].
 struct DecodeGenericArgs {
