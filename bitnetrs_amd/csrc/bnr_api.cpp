@@ -140,7 +140,7 @@ void fingerprint(const uint8_t *p, size_t len, uint8_t *out) {
 constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
-  int n_tokens, start_pos, n_kv, shift;
+  int n_tokens, start_pos, n_kv, tiles;
 };
 
 struct DeviceGuard {
@@ -207,9 +207,9 @@ struct bnr_ctx {
 
   // prefill planner
   int n_cu = 256;
-  int pf_chunk_shift = -1;  // -1: planner decides; else key tiles per chunk = 2^shift
+  int pf_chunk_tiles = -1;  // -1: planner decides; else key tiles per chunk
   int pf_persistent = 0;    // 1: resident workgroups take prefill items from a queue
-  std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> chunk shift) plans
+  std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
 
 namespace {
@@ -285,7 +285,7 @@ int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
 // MI355X spans over 15 shapes x 6 chunk sizes (128 to 8192 tokens, start
 // 0 to 4000; a tile of 4 heads alone on a CU takes about 4 us): they keep
 // the chosen chunk size within 10 % of the best measured one (2 % median).
-double prefill_span(int n_tokens, int start_pos, int n_kv, int shift, int n_cu) {
+double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu) {
   constexpr double kShared = 1.9, kFixed = 1.0, kStore = 0.0, kMerge = 0.1;
   constexpr int kXcd = 8, kSlots = 2;
   const int ncu = std::max(1, n_cu / kXcd);
@@ -335,10 +335,10 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int shift, int n_cu) 
   order.n_tokens = n_tokens;
   order.start_pos = start_pos;
   order.n_qtiles = (n_tokens + 31) / 32;
-  order.chunk_shift = std::min(shift, 20);
+  order.chunk_tiles = std::min(std::max(ctiles_in, 1), kPrefillNoSplit);
   prefill_order(order);
-  const int ctiles = 1 << order.chunk_shift;
-  const int n_items = prefill_plan(n_tokens, start_pos, order.chunk_shift).n_items;
+  const int ctiles = order.chunk_tiles;
+  const int n_items = prefill_plan(n_tokens, start_pos, ctiles).n_items;
   double now = 0.0, span = 0.0;
   long long wg = 0;
   for (int y = 0; y < n_items; ++y) {
@@ -396,19 +396,25 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int shift, int n_cu) 
   return span;
 }
 
-// Chunk shift for a prefill shape (20: no split); the last 16 shapes are
-// remembered, a new one costs a few replays (tens to hundreds of us).
+// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split); the
+// last 16 shapes are remembered, a new one costs a replay per candidate
+// (tens to hundreds of us each).  Sizes between the powers of two matter:
+// they set how evenly the items fill the resident slots (N = 1024 runs 8 %
+// faster at 6 tiles than at 4, 512 queries after 1536 cached 14 % faster at
+// 10 than at 4 or 16).
+constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
+
 int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
   for (const PrefillPlanEntry &e : c->pf_plans)
-    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) return e.shift;
-  int best = 20;
-  double best_span = prefill_span(n_tokens, start_pos, n_kv, 20, c->n_cu);
-  for (int shift = 2; shift <= 6; ++shift) {
-    if (prefill_plan(n_tokens, start_pos, shift).n_items * (long long)n_kv > 8192) continue;
-    const double span = prefill_span(n_tokens, start_pos, n_kv, shift, c->n_cu);
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) return e.tiles;
+  int best = kPrefillNoSplit;
+  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, c->n_cu);
+  for (int ct : kPrefillChunkCandidates) {
+    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > 8192) continue;
+    const double span = prefill_span(n_tokens, start_pos, n_kv, ct, c->n_cu);
     if (span < best_span * 0.99) {
       best_span = span;
-      best = shift;
+      best = ct;
     }
   }
   if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
@@ -682,7 +688,8 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     int r = atoi(v);
     if (r >= 1 && r <= 8) c->force_rpg = r;
   }
-  if (const char *v = std::getenv("BNR_PREFILL_CHUNK_SHIFT")) c->pf_chunk_shift = std::min(std::max(atoi(v), 0), 20);
+  if (const char *v = std::getenv("BNR_PREFILL_CHUNK_TILES"))
+    c->pf_chunk_tiles = std::min(std::max(atoi(v), 1), kPrefillNoSplit);
   if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT")) c->pf_persistent = atoi(v) > 0;
   *out = c;
   return set_ok();
@@ -1272,12 +1279,12 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
     pa.n_kv = (int)n_kv_heads;
     pa.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
     pa.n_qtiles = (int)((n_tokens + 31) / 32);
-    pa.chunk_shift = c->pf_chunk_shift >= 0
-                         ? c->pf_chunk_shift
+    pa.chunk_tiles = c->pf_chunk_tiles > 0
+                         ? c->pf_chunk_tiles
                          : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads);
-    PrefillPlan plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_shift);
+    PrefillPlan plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_tiles);
     while (plan.n_items > 65535)  // grid y limit
-      plan = prefill_plan((int)n_tokens, (int)start_pos, ++pa.chunk_shift);
+      plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_tiles *= 2);
     pa.n_items = plan.n_items;
     prefill_order(pa);
     if (plan.split) {

@@ -98,8 +98,8 @@ struct PrefillArgs {
   int n_tokens, start_pos, n_heads, n_kv;
   float scale_log2;                  // log2(e) / sqrt(128)
   // Key-range split: a query tile's key tiles are processed in chunks of
-  // 2^chunk_shift tiles by separate workgroups; the last to finish merges.
-  int chunk_shift;
+  // chunk_tiles tiles by separate workgroups; the last to finish merges.
+  int chunk_tiles;
   int n_qtiles;                      // ceil(n_tokens / 32)
   int n_items;                       // (query tile, chunk) items per kv head
   float *ws;                         // partial states: [n_kv][n_items][G][66][64], by (query tile, chunk)
@@ -108,22 +108,23 @@ struct PrefillArgs {
   // Item order (prefill_order fills these).  lpt: longest first -- every
   // full-length chunk (n_full of them per kv head), then the shorter last
   // chunks of the query tiles by decreasing length, those of length ct-1-b
-  // at part_off[b] .. part_off[b+1]-1 after the full ones (ct = 2^chunk_shift
+  // at part_off[b] .. part_off[b+1]-1 after the full ones (ct = chunk_tiles
   // <= kMaxLptChunk).  Otherwise query tiles from the last down, the chunks
   // of one tile consecutive.
   int lpt, n_full;
   int part_off[64];
 };
 constexpr int kMaxLptChunk = 64;
+constexpr int kPrefillNoSplit = 1 << 20;  // chunk_tiles of an unsplit launch
 
-// Sum over x = 1..m of floor(x / 2^sh), and of ceil(x / 2^sh) (m >= 0).
-__host__ __device__ inline long long pf_floor_sum(long long m, int sh) {
-  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
-  return q > 0 ? (((q * (q - 1)) >> 1) << sh) + q * (r + 1) : 0;
+// Sum over x = 1..m of floor(x / ct), and of ceil(x / ct) (m >= 0, ct >= 1).
+__host__ __device__ inline long long pf_floor_sum(int m, int ct) {
+  const long long q = m / ct, r = m % ct;
+  return q > 0 ? ct * (q * (q - 1) / 2) + q * (r + 1) : 0;
 }
-__host__ __device__ inline long long pf_ceil_sum(long long m, int sh) {
-  const long long q = m >> sh, r = m & ((1LL << sh) - 1);
-  return ((q * (q + 1) >> 1) << sh) + r * (q + 1);
+__host__ __device__ inline long long pf_ceil_sum(int m, int ct) {
+  const long long q = m / ct, r = m % ct;
+  return ct * (q * (q + 1) / 2) + r * (q + 1);
 }
 
 // Work item y (per kv head) of a prefill launch -> query tile qt, chunk ch
@@ -133,50 +134,50 @@ __host__ __device__ inline long long pf_ceil_sum(long long m, int sh) {
 // last_row / 32 + 1.  The host's dispatch replay uses the same function.
 __host__ __device__ inline void prefill_map(const PrefillArgs &a, int y, int &qt, int &ch,
                                             int &nch, int &base) {
-  const int sh = a.chunk_shift, ct = 1 << sh, nqt = a.n_qtiles;
+  const int ct = a.chunk_tiles, nqt = a.n_qtiles;
   const int last_row = a.start_pos + a.n_tokens - 1;
   const int A = (a.start_pos + 31) / 32 + 1;
   const int nt_last = last_row / 32 + 1;
   if (!a.lpt) {
     // Tiles from the last down, chunks consecutive: the items of tiles
     // q .. nqt-2 are a difference of two ceil sums; binary search.
-    const int nch_last = (nt_last + ct - 1) >> sh;
+    const int nch_last = (nt_last + ct - 1) / ct;
     if (y < nch_last) {
       qt = nqt - 1;
       ch = y;
       nch = nch_last;
     } else {
       const long long yy = y - nch_last;
-      const long long top = pf_ceil_sum(nqt - 2 + A, sh);
+      const long long top = pf_ceil_sum(nqt - 2 + A, ct);
       int lo = 0, hi = nqt - 2;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (top - pf_ceil_sum(mid - 1 + A, sh) > yy) lo = mid;
+        if (top - pf_ceil_sum(mid - 1 + A, ct) > yy) lo = mid;
         else hi = mid - 1;
       }
       qt = lo;
-      ch = (int)(yy - (top - pf_ceil_sum(lo + A, sh)));
-      nch = (lo + A + ct - 1) >> sh;
+      ch = (int)(yy - (top - pf_ceil_sum(lo + A, ct)));
+      nch = (lo + A + ct - 1) / ct;
     }
   } else if (y < a.n_full) {
     // Full chunks: the last tile's, then tiles nqt-2 down to 0 (floor sums).
-    const int f_last = nt_last >> sh;
+    const int f_last = nt_last / ct;
     if (y < f_last) {
       qt = nqt - 1;
       ch = y;
-      nch = (nt_last + ct - 1) >> sh;
+      nch = (nt_last + ct - 1) / ct;
     } else {
       const long long yy = y - f_last;
-      const long long top = pf_floor_sum(nqt - 2 + A, sh);
+      const long long top = pf_floor_sum(nqt - 2 + A, ct);
       int lo = 0, hi = nqt - 2;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (top - pf_floor_sum(mid - 1 + A, sh) > yy) lo = mid;
+        if (top - pf_floor_sum(mid - 1 + A, ct) > yy) lo = mid;
         else hi = mid - 1;
       }
       qt = lo;
-      ch = (int)(yy - (top - pf_floor_sum(lo + A, sh)));
-      nch = (lo + A + ct - 1) >> sh;
+      ch = (int)(yy - (top - pf_floor_sum(lo + A, ct)));
+      nch = (lo + A + ct - 1) / ct;
     }
   } else {
     // Last chunks shorter than ct, longest first; within one length the
@@ -186,12 +187,12 @@ __host__ __device__ inline void prefill_map(const PrefillArgs &a, int y, int &qt
     while (b + 1 < ct - 1 && a.part_off[b + 1] <= y2) ++b;
     const int r = ct - 1 - b;
     int k = y2 - a.part_off[b];
-    if ((nt_last & (ct - 1)) == r) {
+    if (nt_last % ct == r) {
       if (k == 0) {
         qt = nqt - 1;
-        ch = nt_last >> sh;
+        ch = nt_last / ct;
         nch = ch + 1;
-        base = (int)(pf_ceil_sum(qt - 1 + A, sh) - pf_ceil_sum(A - 1, sh));
+        base = (int)(pf_ceil_sum(qt - 1 + A, ct) - pf_ceil_sum(A - 1, ct));
         return;
       }
       --k;
@@ -199,10 +200,10 @@ __host__ __device__ inline void prefill_map(const PrefillArgs &a, int y, int &qt
     const int q0 = ((r - A) % ct + ct) % ct;  // lowest regular tile with qt + A = r (mod ct)
     const int cnt = nqt - 2 >= q0 ? (nqt - 2 - q0) / ct + 1 : 0;
     qt = q0 + (cnt - 1 - k) * ct;
-    ch = (qt + A) >> sh;
+    ch = (qt + A) / ct;
     nch = ch + 1;
   }
-  base = (int)(pf_ceil_sum(qt - 1 + A, sh) - pf_ceil_sum(A - 1, sh));
+  base = (int)(pf_ceil_sum(qt - 1 + A, ct) - pf_ceil_sum(A - 1, ct));
 }
 
 // (query tile, chunk) items per kv head of a prefill launch, and the key
@@ -212,9 +213,9 @@ struct PrefillPlan {
   long long key_tiles;
   bool split;  // some query tile has more than one chunk
 };
-PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift);
+PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_tiles);
 // Fills a.lpt, a.n_full and a.part_off from a.n_tokens, a.start_pos,
-// a.n_qtiles and a.chunk_shift.
+// a.n_qtiles and a.chunk_tiles.
 void prefill_order(PrefillArgs &a);
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.
 hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, hipStream_t s);

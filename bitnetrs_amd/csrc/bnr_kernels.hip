@@ -715,7 +715,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
 // query: a key tile's max and sum are the lane's 16 values plus its partner
 // lane l^32.
 //
-// Long query tiles are cut into key chunks of 2^chunk_shift tiles (separate
+// Long query tiles are cut into key chunks of chunk_tiles tiles (separate
 // workgroups); the last chunk of a tile to finish merges the others' partial
 // states.  Work items are dispatched longest query tile first.
 // ---------------------------------------------------------------------------
@@ -753,8 +753,8 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
   prefill_map(a, y, it.qt, it.ch, it.nch, it.base);
   it.q0 = it.qt * 32;
   const int kmax = min(a.start_pos + it.q0 + 31, last_row);
-  it.kt0 = it.ch << a.chunk_shift;
-  it.nkt = min(kmax / 32 + 1, it.kt0 + (1 << a.chunk_shift));
+  it.kt0 = it.ch * a.chunk_tiles;
+  it.nkt = min(kmax / 32 + 1, it.kt0 + a.chunk_tiles);
   return it;
 }
 
@@ -1196,7 +1196,7 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
 bool prefill_supported(int group) { return group == 2 || group == 4 || group == 8; }
 
 void prefill_order(PrefillArgs &a) {
-  const int sh = a.chunk_shift, ct = 1 << sh, nqt = a.n_qtiles;
+  const int ct = a.chunk_tiles, nqt = a.n_qtiles;
   const int last_row = a.start_pos + a.n_tokens - 1;
   const int A = (a.start_pos + 31) / 32 + 1;
   const int nt_last = last_row / 32 + 1;
@@ -1205,23 +1205,23 @@ void prefill_order(PrefillArgs &a) {
   for (int b = 0; b < kMaxLptChunk; ++b) a.part_off[b] = 0;
   if (!a.lpt) return;
   int count[kMaxLptChunk] = {};  // last chunks of length r (< ct)
-  a.n_full = nt_last >> sh;
-  count[nt_last & (ct - 1)] += 1;
+  a.n_full = nt_last / ct;
+  count[nt_last % ct] += 1;
   for (int qt = 0; qt + 1 < nqt; ++qt) {
-    a.n_full += (qt + A) >> sh;
-    count[(qt + A) & (ct - 1)] += 1;
+    a.n_full += (qt + A) / ct;
+    count[(qt + A) % ct] += 1;
   }
   // bucket b holds length ct-1-b; part_off[b] = items of longer buckets
   for (int b = 1; b < ct; ++b) a.part_off[b] = a.part_off[b - 1] + count[ct - b];
 }
 
-PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_shift) {
+PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_tiles) {
   const int last_row = start_pos + n_tokens - 1, nqt = (n_tokens + 31) / 32;
-  const int ctiles = 1 << chunk_shift;
+  const int ctiles = chunk_tiles;
   PrefillPlan p{0, 0, false};
   for (int qt = 0; qt < nqt; ++qt) {
     const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
-    const int nch = (nk + ctiles - 1) >> chunk_shift;
+    const int nch = (nk + ctiles - 1) / ctiles;
     p.n_items += nch;
     p.key_tiles += nk;
     p.split |= nch > 1;

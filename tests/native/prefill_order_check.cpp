@@ -11,14 +11,14 @@
 
 using namespace bnr;
 
-static int check(int n_tokens, int start_pos, int shift) {
+static int check(int n_tokens, int start_pos, int ct) {
   PrefillArgs a{};
   a.n_tokens = n_tokens;
   a.start_pos = start_pos;
   a.n_qtiles = (n_tokens + 31) / 32;
-  a.chunk_shift = shift;
+  a.chunk_tiles = ct;
   prefill_order(a);
-  const int ct = 1 << shift, nqt = a.n_qtiles, last_row = start_pos + n_tokens - 1;
+  const int nqt = a.n_qtiles, last_row = start_pos + n_tokens - 1;
   std::vector<int> nt(nqt), nchs(nqt), base(nqt);
   int total = 0;
   for (int qt = 0; qt < nqt; ++qt) {
@@ -27,7 +27,7 @@ static int check(int n_tokens, int start_pos, int shift) {
     base[qt] = total;
     total += nchs[qt];
   }
-  if (total != prefill_plan(n_tokens, start_pos, shift).n_items) return 1;
+  if (total != prefill_plan(n_tokens, start_pos, ct).n_items) return 1;
   std::vector<int> seen(total, 0);
   int prev_len = 1 << 30;
   for (int y = 0; y < total; ++y) {
@@ -49,11 +49,11 @@ int main() {
   const int starts[] = {0, 1, 5, 31, 32, 33, 200, 1000, 1536, 4095};
   for (int n : ns)
     for (int st : starts)
-      for (int sh = 0; sh <= 20; sh = sh < 7 ? sh + 1 : sh + 13) {
-        const int r = check(n, st, sh);
+      for (int ct : {1, 2, 3, 4, 5, 6, 7, 8, 10, 12, 16, 24, 32, 48, 64, 100, kPrefillNoSplit}) {
+        const int r = check(n, st, ct);
         ++shapes;
         if (r) {
-          std::printf("fail %d: n_tokens %d start_pos %d shift %d\n", r, n, st, sh);
+          std::printf("fail %d: n_tokens %d start_pos %d chunk_tiles %d\n", r, n, st, ct);
           return 1;
         }
       }

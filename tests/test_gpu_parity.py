@@ -386,19 +386,20 @@ def test_dev_prefill_shapes(backend, n_heads, n_kv, n_tokens, start):
     assert_close(host(out), out_ref, f"prefill {n_heads}/{n_kv} n {n_tokens}")
 
 
-@pytest.mark.parametrize("shift,persistent", [(0, 0), (1, 0), (3, 0), (1, 1), (3, 1), (20, 1)])
-def test_dev_prefill_key_chunks(monkeypatch, shift, persistent):
-    """Query tiles cut into key chunks of 2^shift tiles (merged by the last
+@pytest.mark.parametrize("tiles,persistent", [(1, 0), (2, 0), (3, 0), (5, 0), (8, 0), (2, 1), (3, 1),
+                                               (8, 1), (1 << 20, 1)])
+def test_dev_prefill_key_chunks(monkeypatch, tiles, persistent):
+    """Query tiles cut into key chunks of `tiles` key tiles (merged by the last
     chunk to finish), at start positions that are not tile-aligned so some
     chunks see no key at all for their first queries; two prefills in a row
     check that the merge tickets (and, persistent, the item queue) reset
     themselves.  persistent: resident workgroups take items from a queue."""
-    case(f"prefill key chunks shift {shift} persistent {persistent}")
+    case(f"prefill key chunks tiles {tiles} persistent {persistent}")
     import torch
 
     import bitnetrs_amd
 
-    monkeypatch.setenv("BNR_PREFILL_CHUNK_SHIFT", str(shift))
+    monkeypatch.setenv("BNR_PREFILL_CHUNK_TILES", str(tiles))
     monkeypatch.setenv("BNR_PREFILL_PERSISTENT", str(persistent))
     be_gpu = bitnetrs_amd.HipBackend(0)
     try:
@@ -418,7 +419,7 @@ def test_dev_prefill_key_chunks(monkeypatch, shift, persistent):
             out = torch.zeros(n_tokens, HQ * D, device="cuda")
             be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, HQ, HKV, D,
                                THETA, d_kc, d_vc, cap, out)
-            assert_close(host(out), out_ref, f"prefill chunks 2^{shift} n {n_tokens} start {start}")
+            assert_close(host(out), out_ref, f"prefill chunks of {tiles} n {n_tokens} start {start}")
             start += n_tokens
     finally:
         be_gpu.close()

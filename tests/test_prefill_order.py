@@ -3,7 +3,8 @@ kernels and the host planner's dispatch replay) is a bijection onto the
 (query tile, key chunk) pairs, with the chunk counts and partial-state slots
 the merge expects, and with non-increasing chunk lengths in the
 longest-first order.  A host-only harness is built with hipcc against the
-library and run over 1350 shapes (no GPU needed)."""
+library and run over 2550 shapes (150 launch shapes x 17 chunk sizes, no GPU
+needed)."""
 import os
 import shutil
 import subprocess
