@@ -1265,8 +1265,11 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
   const long long qs = (long long)(n_heads * head_dim);
   const long long kv_stride = (long long)(cap * head_dim);
   const int group = (int)(n_heads / n_kv_heads);
+  // The tiled kernel takes at most 65535 query tiles (its grid's y extent)
+  // and int positions; longer launches run as per-row decodes below.
   if (head_dim == (size_t)kHeadDim && prefill_supported(group) && aligned16(q) &&
-      aligned16(k_cache) && aligned16(v_cache) && aligned16(out)) {
+      aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
+      n_tokens <= (size_t)kPrefillMaxTokens && start_pos + n_tokens <= (size_t)INT32_MAX) {
     PrefillArgs pa{};
     pa.q = q;
     pa.k_cache = k_cache;

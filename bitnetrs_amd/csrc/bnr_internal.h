@@ -116,6 +116,7 @@ struct PrefillArgs {
 };
 constexpr int kMaxLptChunk = 64;
 constexpr int kPrefillNoSplit = 1 << 20;  // chunk_tiles of an unsplit launch
+constexpr int kPrefillMaxTokens = 32 * 65535;  // query tiles of one tiled prefill launch
 
 // Sum over x = 1..m of floor(x / ct), and of ceil(x / ct) (m >= 0, ct >= 1).
 __host__ __device__ inline long long pf_floor_sum(int m, int ct) {
