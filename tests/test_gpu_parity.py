@@ -423,3 +423,43 @@ def test_dev_prefill_key_chunks(monkeypatch, tiles, persistent):
             start += n_tokens
     finally:
         be_gpu.close()
+
+
+@pytest.mark.parametrize("n_heads,n_kv,tiles,persistent", [(16, 2, 2, 0), (16, 2, 3, 1),
+                                                           (8, 4, 3, 0), (8, 4, 2, 1)])
+def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persistent):
+    """Key-chunk merges with 8 and 2 query heads per kv head (8 and 2 waves
+    per workgroup; the persistent kernel keeps one workgroup of 8 waves per
+    CU): 230 queries after 45 cached rows, two launches in a row."""
+    case(f"prefill key chunks heads {n_heads}/{n_kv} tiles {tiles} persistent {persistent}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_CHUNK_TILES", str(tiles))
+    monkeypatch.setenv("BNR_PREFILL_PERSISTENT", str(persistent))
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = 520
+        cache = oracle.KVCache(1, n_kv, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        pre = prefill_workload(40, 45, n_heads, n_kv)
+        oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+        start = 45
+        for n_tokens, s in ((230, 41), (200, 42)):
+            w = prefill_workload(s, n_tokens, n_heads, n_kv)
+            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
+                                                  n_heads=n_heads, n_kv=n_kv)
+            out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+                               n_kv, D, THETA, d_kc, d_vc, cap, out)
+            np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+            assert_close(host(out), out_ref,
+                         f"prefill {n_heads}/{n_kv} chunks of {tiles} n {n_tokens} start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
