@@ -153,6 +153,15 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `make -C {CSRC}` "
                 "(or __graft_entry__.build()); there is no fallback path")
+        # PyTorch wheels bundle their own HIP runtime, which the dynamic
+        # loader also hands to this library (libamdhip64.so.7) when torch is
+        # loaded first: one runtime then serves tensors and library calls.
+        # Loaded the other way round, the process holds two runtimes and
+        # torch finds no GPU.  So torch, when installed, goes first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         lib = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

@@ -190,6 +190,8 @@ struct bnr_ctx {
   // host-path staging
   float *d_q = nullptr, *d_k = nullptr, *d_out = nullptr;
   size_t d_q_n = 0, d_k_n = 0, d_out_n = 0;
+  float *h_stage = nullptr;  // pinned host staging of the host-slice calls
+  size_t h_stage_n = 0;
 
   // mirrors, most recently used first
   std::list<Mirror> mirrors;
@@ -232,6 +234,26 @@ int ensure_buf(float **p, size_t *cap, size_t n, const char *what) {
   size_t want = std::max<size_t>(n, 1024);
   HIP_TRY(hipMalloc((void **)p, want * sizeof(float)), what);
   *cap = want;
+  return BNR_OK;
+}
+
+size_t round4(size_t n) { return (n + 3) & ~(size_t)3; }
+
+// Grow-only pinned host buffer.  The host-slice entry points gather their
+// slices into it and move them with one DMA copy each way; a pageable copy
+// pays a staging round trip of its own for every slice.
+int ensure_host(bnr_ctx *c, size_t n) {
+  if (c->h_stage_n >= n && c->h_stage) return BNR_OK;
+  if (c->h_stage) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipHostFree(c->h_stage);
+    c->h_stage = nullptr;
+    c->h_stage_n = 0;
+  }
+  const size_t want = std::max<size_t>(n, 16384);
+  HIP_TRY(hipHostMalloc((void **)&c->h_stage, want * sizeof(float), hipHostMallocDefault),
+          "pinned staging alloc");
+  c->h_stage_n = want;
   return BNR_OK;
 }
 
@@ -473,7 +495,14 @@ int ensure_table(bnr_ctx *c, size_t position, size_t head_dim, float theta) {
   const bool reinit = !c->tab_valid || c->tab_head_dim != head_dim ||
                       std::fabs(c->tab_theta - theta) > 1e-3f || position >= c->tab_len;
   if (!reinit) return BNR_OK;
-  return build_table(c, std::max<size_t>(position + 1, 4096), head_dim, theta);
+  size_t len = std::max<size_t>(position + 1, 4096);
+  // A position past the end of a table of the same head_dim and theta grows
+  // it geometrically.  Entries depend on (position, i) only, so every value
+  // is the one the reference's max(position + 1, 4096) table holds; only the
+  // rebuild on every call past the end is saved.
+  if (c->tab_valid && c->tab_head_dim == head_dim && std::fabs(c->tab_theta - theta) <= 1e-3f)
+    len = std::max(len, 2 * c->tab_len);
+  return build_table(c, len, head_dim, theta);
 }
 
 bool fast_shape(size_t n_heads, size_t n_kv, size_t head_dim) {
@@ -705,6 +734,7 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     for (auto &m : c->weight_mirrors)
       if (m.dev) (void)hipFree(m.dev);
     if (c->d_bytes) (void)hipFree(c->d_bytes);
+    if (c->h_stage) (void)hipHostFree(c->h_stage);
     float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out, c->pf_ws};
     for (float *p : bufs)
       if (p) (void)hipFree(p);
@@ -741,15 +771,19 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
                      fmt("k.len() = %zu", k_len));
   if (q_len + k_len == 0) return set_ok();
   if ((q_len && !q) || (k_len && !k)) return err_backend("rope_embed: NULL slice");
-  st = ensure_buf(&c->d_q, &c->d_q_n, q_len + 1, "staging alloc");
+  // q and k in one pinned copy each way: [q | k], k 16-byte aligned.
+  const size_t qs = round4(q_len), total = qs + k_len;
+  st = ensure_buf(&c->d_q, &c->d_q_n, total, "staging alloc");
   if (st) return st;
-  st = ensure_buf(&c->d_k, &c->d_k_n, k_len + 1, "staging alloc");
+  st = ensure_host(c, total);
   if (st) return st;
-  if (q_len) HIP_TRY(hipMemcpyAsync(c->d_q, q, q_len * 4, hipMemcpyHostToDevice, c->stream), "upload q");
-  if (k_len) HIP_TRY(hipMemcpyAsync(c->d_k, k, k_len * 4, hipMemcpyHostToDevice, c->stream), "upload k");
+  float *h = c->h_stage;
+  if (q_len) std::memcpy(h, q, q_len * sizeof(float));
+  if (k_len) std::memcpy(h + qs, k, k_len * sizeof(float));
+  HIP_TRY(hipMemcpyAsync(c->d_q, h, total * 4, hipMemcpyHostToDevice, c->stream), "upload q/k");
   RopeAppendArgs a{};
   a.q = c->d_q;
-  a.k = c->d_k;
+  a.k = c->d_q + qs;
   a.n_tokens = 1;
   a.start_pos = (int)position;
   a.n_heads = (int)n_heads;
@@ -758,9 +792,10 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
   a.cos_tab = c->d_cos;
   a.sin_tab = c->d_sin;
   HIP_TRY(launch_rope_append(a, c->stream), "rope launch");
-  if (q_len) HIP_TRY(hipMemcpyAsync(q, c->d_q, q_len * 4, hipMemcpyDeviceToHost, c->stream), "download q");
-  if (k_len) HIP_TRY(hipMemcpyAsync(k, c->d_k, k_len * 4, hipMemcpyDeviceToHost, c->stream), "download k");
+  HIP_TRY(hipMemcpyAsync(h, c->d_q, total * 4, hipMemcpyDeviceToHost, c->stream), "download q/k");
   HIP_TRY(hipStreamSynchronize(c->stream), "rope_embed");
+  if (q_len) std::memcpy(q, h, q_len * sizeof(float));
+  if (k_len) std::memcpy(k, h + qs, k_len * sizeof(float));
   return set_ok();
 }
 
@@ -826,6 +861,41 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
   }
   size_t r0 = 0;
   if (c->mirror_mode == BNR_MIRROR_INCREMENTAL && m->synced == cur_pos) r0 = cur_pos;
+  if (r0 == cur_pos && cur_pos > 0 && fast_shape(n_heads, n_kv_heads, head_dim)) {
+    // One new row: q and row cur_pos of every kv head go over in one pinned
+    // copy, and the decode kernel appends the row to the mirror itself
+    // (fused append, no rotation).  Device staging: [q | k row | v row | out].
+    const size_t rs = n_kv_heads * head_dim, in_n = q_len + 2 * rs;
+    int st = ensure_buf(&c->d_q, &c->d_q_n, in_n + out_len, "staging alloc");
+    if (st) return st;
+    st = ensure_host(c, std::max(in_n, out_len));
+    if (st) return st;
+    float *h = c->h_stage, *d = c->d_q;
+    std::memcpy(h, q, q_len * sizeof(float));
+    for (size_t kh = 0; kh < n_kv_heads; ++kh) {
+      const size_t src = kh * head_stride + cur_pos * head_dim;
+      std::memcpy(h + q_len + kh * head_dim, k_cache + src, head_dim * sizeof(float));
+      std::memcpy(h + q_len + rs + kh * head_dim, v_cache + src, head_dim * sizeof(float));
+    }
+    m->synced = 0;  // unknown until the launch and the copies succeed
+    HIP_TRY(hipMemcpyAsync(d, h, in_n * 4, hipMemcpyHostToDevice, c->stream), "upload q/row");
+    DecodeArgs a{};
+    a.q = d;
+    a.k_new = d + q_len;
+    a.v_new = d + q_len + rs;
+    a.k_cache = m->dk;
+    a.v_cache = m->dv;
+    a.kv_stride = (long long)(m->rows * head_dim);
+    a.out = d + in_n;
+    const int p = (int)cur_pos;
+    st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), m->rows, c->stream);
+    if (st) return st;
+    HIP_TRY(hipMemcpyAsync(h, d + in_n, out_len * 4, hipMemcpyDeviceToHost, c->stream), "download out");
+    HIP_TRY(hipStreamSynchronize(c->stream), "masked_attention");
+    std::memcpy(output, h, out_len * sizeof(float));
+    m->synced = seq_len;
+    return set_ok();
+  }
   const size_t dpitch = m->rows * head_dim * sizeof(float);
   const size_t spitch = head_stride * sizeof(float);
   const size_t width = (seq_len - r0) * head_dim * sizeof(float);
@@ -1780,8 +1850,6 @@ void kv_mark_stored(bnr_kv_cache *kc, size_t layer, size_t position, size_t n) {
   kc->layer_len[layer] = std::max(kc->layer_len[layer], position + n);
 }
 
-size_t round4(size_t n) { return (n + 3) & ~(size_t)3; }
-
 }  // namespace
 
 extern "C" int bnr_kv_cache_create(bnr_ctx *c, size_t n_layers, size_t n_kv_heads, size_t head_dim,
@@ -1907,24 +1975,29 @@ extern "C" int bnr_kv_decode(bnr_ctx *c, bnr_kv_cache *kc, size_t layer, float *
   if (kc->device != c->device) return err_backend("kv cache and context are on different devices");
   std::lock_guard<std::mutex> lc(c->mu);
   DeviceGuard dg(c->device);
-  // Staging: q, k, v in; rotated q, rotated k and the output back.
-  const size_t qs = round4(q_len), ks = round4(kvn);
-  st = ensure_buf(&c->d_q, &c->d_q_n, 2 * qs + 3 * ks, "staging alloc");
+  // Staging, one pinned copy each way: [q | k | v] in, then [out | rotated q
+  // | rotated k] back, every part 16-byte aligned.
+  const size_t qs = round4(q_len), ks = round4(kvn), os = round4(out_len);
+  const size_t in_n = qs + 2 * ks, back_n = os + qs + ks;
+  st = ensure_buf(&c->d_q, &c->d_q_n, in_n + back_n, "staging alloc");
   if (st) return st;
-  st = ensure_buf(&c->d_out, &c->d_out_n, out_len, "staging alloc");
+  st = ensure_host(c, std::max(in_n, back_n));
   if (st) return st;
-  float *dq = c->d_q, *dk = dq + qs, *dv = dk + ks, *dqr = dv + ks, *dkr = dqr + qs;
-  HIP_TRY(hipMemcpyAsync(dq, q, q_len * 4, hipMemcpyHostToDevice, c->stream), "upload q");
-  HIP_TRY(hipMemcpyAsync(dk, k, kvn * 4, hipMemcpyHostToDevice, c->stream), "upload k");
-  HIP_TRY(hipMemcpyAsync(dv, v, kvn * 4, hipMemcpyHostToDevice, c->stream), "upload v");
+  float *h = c->h_stage;
+  std::memcpy(h, q, q_len * sizeof(float));
+  std::memcpy(h + qs, k, kvn * sizeof(float));
+  std::memcpy(h + qs + ks, v, kvn * sizeof(float));
+  float *dq = c->d_q, *dk = dq + qs, *dv = dk + ks, *dout = dq + in_n, *dqr = dout + os,
+        *dkr = dqr + qs;
+  HIP_TRY(hipMemcpyAsync(dq, h, in_n * 4, hipMemcpyHostToDevice, c->stream), "upload q/k/v");
   st = decode_step_locked(c, dq, dk, dv, position, n_heads, nkv, hd, theta, kc->k(layer),
-                          kc->v(layer), kc->max_seq, c->d_out, dqr, dkr, c->stream);
+                          kc->v(layer), kc->max_seq, dout, dqr, dkr, c->stream);
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(output, c->d_out, out_len * 4, hipMemcpyDeviceToHost, c->stream),
-          "download out");
-  HIP_TRY(hipMemcpyAsync(q, dqr, q_len * 4, hipMemcpyDeviceToHost, c->stream), "download q");
-  HIP_TRY(hipMemcpyAsync(k, dkr, kvn * 4, hipMemcpyDeviceToHost, c->stream), "download k");
+  HIP_TRY(hipMemcpyAsync(h, dout, back_n * 4, hipMemcpyDeviceToHost, c->stream), "download");
   HIP_TRY(hipStreamSynchronize(c->stream), "kv_decode");
+  std::memcpy(output, h, out_len * sizeof(float));
+  std::memcpy(q, h + os, q_len * sizeof(float));
+  std::memcpy(k, h + os + qs, kvn * sizeof(float));
   kv_mark_stored(kc, layer, position, 1);
   return set_ok();
 }

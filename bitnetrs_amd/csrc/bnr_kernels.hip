@@ -431,8 +431,9 @@ void decode_kernel(DecodeArgs a) {
     qhi[g] = scale4(a.scale_log2, qhi[g]);
   }
 
-  // ---- the new token's rotated key (fused append) ----
-  if (need_new) {
+  // ---- the new token's rotated key (fused append; without a table the row
+  // is appended as given) ----
+  if (need_new && rope) {
     rot4(nklo, nkhi, cs, sn, nklo, nkhi);
     if (a.k_rot && s == 0 && rg == 0) {
       float *kr = a.k_rot + b * a.kn_bstride + h * D;

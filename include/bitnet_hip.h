@@ -70,7 +70,9 @@ const char *bnr_device_name(const bnr_ctx *ctx);
  * `position` with the half-split pairing (i, i+head_dim/2).  The cos/sin
  * table is built on the host with the reference formula and kept in HBM;
  * it is rebuilt when head_dim changes, |theta - cached| > 1e-3 or
- * position >= its length (new length max(position+1, 4096)).  Errors:
+ * position >= its length (new length max(position+1, 4096), at least twice
+ * the old one when only the position ran past it; the entries are the same
+ * either way).  Errors:
  * zero/odd head_dim or non-positive/non-finite theta -> INVALID_CONFIG;
  * wrong q or k length -> INVALID_SHAPE. */
 int bnr_rope_embed(bnr_ctx *ctx, float *q, size_t q_len, float *k, size_t k_len,

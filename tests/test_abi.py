@@ -1,5 +1,6 @@
 """The C-ABI library loads (no GPU needed) and exports every function the
 public header declares; the ctypes table matches the header."""
+import ast
 import ctypes
 import os
 import re
@@ -73,3 +74,16 @@ def test_integration_rust_extern_block_matches_header():
     block = text.split("extern \"C\" {", 1)[1].split("\n}\n", 1)[0]
     rust = sorted(set(re.findall(r"fn (bnr_\w+)\s*\(", block)))
     assert rust == header_functions()
+
+
+def test_one_hip_runtime_after_load():
+    """Loading the library in a fresh process leaves one HIP runtime mapped
+    (torch's bundled one serves the library too), so torch still sees the GPU
+    after the library was loaded first.  No GPU is touched."""
+    code = ("import sys; sys.path.insert(0, %r); import bitnetrs_amd; bitnetrs_amd.load(); "
+            "print(sorted({l.split()[-1] for l in open('/proc/self/maps') if 'libamdhip64' in l}))"
+            % os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    out = subprocess.run(["python3", "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    maps = ast.literal_eval(out.stdout.strip().splitlines()[-1])
+    assert len(maps) == 1, maps
