@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <list>
 #include <mutex>
 #include <new>
@@ -254,6 +255,38 @@ int ensure_host(bnr_ctx *c, size_t n) {
   HIP_TRY(hipHostMalloc((void **)&c->h_stage, want * sizeof(float), hipHostMallocDefault),
           "pinned staging alloc");
   c->h_stage_n = want;
+  return BNR_OK;
+}
+
+// Host slices to device memory through the pinned buffer: the parts are
+// packed back to back and sent with one DMA copy.  The packing is not
+// ordered with the stream, so a call uploads once before get_host.
+struct HostPart {
+  const void *src;
+  size_t bytes;
+};
+int put_host(bnr_ctx *c, void *dev, std::initializer_list<HostPart> parts, const char *what) {
+  size_t total = 0;
+  for (const HostPart &p : parts) total += p.bytes;
+  int st = ensure_host(c, (total + 3) / 4);
+  if (st) return st;
+  char *h = reinterpret_cast<char *>(c->h_stage);
+  for (const HostPart &p : parts) {
+    if (p.bytes) std::memcpy(h, p.src, p.bytes);
+    h += p.bytes;
+  }
+  HIP_TRY(hipMemcpyAsync(dev, c->h_stage, total, hipMemcpyHostToDevice, c->stream), what);
+  return BNR_OK;
+}
+
+// A device range into a host slice through the pinned buffer.  Waits for
+// the stream: the host entry points return with their outputs written.
+int get_host(bnr_ctx *c, void *host, const void *dev, size_t bytes, const char *what) {
+  int st = ensure_host(c, (bytes + 3) / 4);
+  if (st) return st;
+  HIP_TRY(hipMemcpyAsync(c->h_stage, dev, bytes, hipMemcpyDeviceToHost, c->stream), what);
+  HIP_TRY(hipStreamSynchronize(c->stream), what);
+  std::memcpy(host, c->h_stage, bytes);
   return BNR_OK;
 }
 
@@ -1083,16 +1116,15 @@ extern "C" int bnr_ternary_gemv_preq(bnr_ctx *c, const uint8_t *weight_packed, s
   }
   st = ensure_buf(&c->d_out, &c->d_out_n, out_features, "staging alloc");
   if (st) return st;
-  if (in_features)
-    HIP_TRY(hipMemcpyAsync(c->d_bytes, activation_q, in_features, hipMemcpyHostToDevice, c->stream),
-            "upload activation");
+  if (in_features) {
+    st = put_host(c, c->d_bytes, {{activation_q, in_features}}, "upload activation");
+    if (st) return st;
+  }
   st = run_gemv(dw, weight_scale, (const int8_t *)c->d_bytes, act_absmax, c->d_out, out_features,
                 in_features, c->stream);
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(output, c->d_out, out_features * 4, hipMemcpyDeviceToHost, c->stream),
-          "download output");
-  HIP_TRY(hipStreamSynchronize(c->stream), "ternary_gemv_preq");
-  return set_ok();
+  st = get_host(c, output, c->d_out, out_features * 4, "ternary_gemv_preq");
+  return st ? st : set_ok();
 }
 
 // ---------------------------------------------------------------------------
@@ -1482,16 +1514,15 @@ extern "C" int bnr_lm_head_matmul_i8_into(bnr_ctx *c, const float *hidden, size_
   if (st) return st;
   st = ensure_buf(&c->d_out, &c->d_out_n, vocab_size, "staging alloc");
   if (st) return st;
-  if (hidden_size)
-    HIP_TRY(hipMemcpyAsync(c->d_q, hidden, hidden_size * 4, hipMemcpyHostToDevice, c->stream),
-            "upload hidden");
+  if (hidden_size) {
+    st = put_host(c, c->d_q, {{hidden, hidden_size * 4}}, "upload hidden");
+    if (st) return st;
+  }
   st = run_lm_head(c->d_q, (const int8_t *)dw, (const float *)dsc, c->d_out, vocab_size,
                    hidden_size, c->stream);
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(output, c->d_out, vocab_size * 4, hipMemcpyDeviceToHost, c->stream),
-          "download output");
-  HIP_TRY(hipStreamSynchronize(c->stream), "lm_head_matmul_i8_into");
-  return set_ok();
+  st = get_host(c, output, c->d_out, vocab_size * 4, "lm_head_matmul_i8_into");
+  return st ? st : set_ok();
 }
 
 extern "C" int bnr_dev_lm_head_matmul_i8(bnr_ctx *c, const float *hidden, const int8_t *weights_i8,
@@ -1705,13 +1736,13 @@ extern "C" int bnr_rms_norm(bnr_ctx *c, const float *input, size_t in_len, const
   if (st) return st;
   st = ensure_buf(&c->d_out, &c->d_out_n, in_len, "staging alloc");
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(c->d_q, input, in_len * 4, hipMemcpyHostToDevice, c->stream), "upload input");
+  st = put_host(c, c->d_q, {{input, in_len * 4}}, "upload input");
+  if (st) return st;
   st = run_norm_quant(c, kGluePlain, c->d_q, nullptr, (const float *)dw, eps, in_len, nullptr,
                       c->d_out, nullptr, nullptr, nullptr, c->stream);
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(output, c->d_out, in_len * 4, hipMemcpyDeviceToHost, c->stream), "download output");
-  HIP_TRY(hipStreamSynchronize(c->stream), "rms_norm");
-  return set_ok();
+  st = get_host(c, output, c->d_out, in_len * 4, "rms_norm");
+  return st ? st : set_ok();
 }
 
 extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, const float *up,
@@ -1728,12 +1759,11 @@ extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, cons
   if (st) return st;
   st = ensure_buf(&c->d_out, &c->d_out_n, g_len, "staging alloc");
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(c->d_q, gate, g_len * 4, hipMemcpyHostToDevice, c->stream), "upload gate");
-  HIP_TRY(hipMemcpyAsync(c->d_q + g_len, up, g_len * 4, hipMemcpyHostToDevice, c->stream), "upload up");
+  st = put_host(c, c->d_q, {{gate, g_len * 4}, {up, g_len * 4}}, "upload gate/up");
+  if (st) return st;
   HIP_TRY(launch_sqrelu(c->d_q, c->d_q + g_len, c->d_out, (long long)g_len, c->stream), "sqrelu launch");
-  HIP_TRY(hipMemcpyAsync(out, c->d_out, g_len * 4, hipMemcpyDeviceToHost, c->stream), "download out");
-  HIP_TRY(hipStreamSynchronize(c->stream), "sqrelu_gate");
-  return set_ok();
+  st = get_host(c, out, c->d_out, g_len * 4, "sqrelu_gate");
+  return st ? st : set_ok();
 }
 
 extern "C" int bnr_dev_rms_norm(bnr_ctx *c, const float *input, const float *weight, float eps,
