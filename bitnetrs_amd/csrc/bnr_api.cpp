@@ -179,6 +179,8 @@ struct bnr_ctx {
   size_t ws_ml_n = 0;
   unsigned *counters = nullptr;
   size_t n_counters = 0;
+  float *acc = nullptr;  // reference-merge accumulators (zero between launches)
+  size_t acc_floats = 0;
   float *scratch = nullptr;  // generic-kernel scores and host-path staging
   size_t scratch_floats = 0;
   float *pf_ws = nullptr;  // prefill chunk partials
@@ -206,7 +208,9 @@ struct bnr_ctx {
   int large_wgs = 1024;
   int force_rpg = 0;
   int min_passes = 1;
-  int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel
+  int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel ticket; 2: reference merge
+  int split_cost = -1;  // planner cost of a split of the in-kernel merges (ns); -1: mode default
+  int ref_rows = 0;     // reference merge: rows per split (0: planner)
 
   // prefill planner
   int n_cu = 256;
@@ -556,13 +560,67 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
   long long wgs4 = 0;  // workgroups at 64 rows each
   for (int b = 0; b < batch; ++b) wgs4 += (lens[b] + 63) / 64;
   wgs4 *= n_kv;
-  // Large launches (several workgroups per CU): 64-row splits, merged by a
-  // second kernel, so that workgroups never wait on their partial stores.
-  // Small launches: merged in-kernel by the last workgroup.  A single
-  // sequence never takes the large path: its parallelism is the splits.
+  // Large launches: several workgroups per CU (batch > 1 and at least
+  // large_wgs splits of 64 rows).  A single sequence never takes the large
+  // path: its parallelism is the splits.  Merge modes: the reference merge
+  // (default, decode_reg_kernel); for the deterministic decode_kernel, the
+  // last workgroup's ticket merge (small launches) or a second kernel
+  // (large ones).
   const bool large = batch > 1 && wgs4 >= c->large_wgs;
-  a.merge_inline = c->merge_mode >= 0 ? c->merge_mode : (large ? 0 : 1);
+  const int mode = c->merge_mode >= 0 ? c->merge_mode : 2;
+  a.merge_inline = mode != 0;
+  a.merge_ref = mode == 2;
+  const long long split_cost = c->split_cost >= 0 ? c->split_cost : 61;
   int passes = 1;
+  if (a.merge_ref) {
+    // Reference merge: the merge cost does not grow with the split count, so
+    // a launch takes the fewest rows per split whose workgroups fit its
+    // target: one round of one workgroup per CU (target_wgs) for a small
+    // launch, eight workgroups per CU (two resident at rpg 4) for a large
+    // one.  A split is a contiguous range of rows of one (sequence, kv head)
+    // in passes of 16 * rpg rows (rpg up to 6; 4 for large launches).
+    const long long target = large ? 8LL * c->target_wgs : c->target_wgs;
+    int max_len = 1;
+    long long total = 0;
+    for (int b = 0; b < batch; ++b) {
+      max_len = std::max(max_len, lens[b]);
+      total += lens[b];
+    }
+    int rows = c->ref_rows;
+    if (rows <= 0) {
+      // smallest rows in [lo, max_len] with sum_b ceil(lens[b] / rows) * n_kv
+      // <= target (non-increasing in rows)
+      auto fits = [&](int r) {
+        long long wgs = 0;
+        for (int b = 0; b < batch; ++b) wgs += (lens[b] + r - 1) / r;
+        return wgs * n_kv <= target;
+      };
+      int lo = (int)std::max<long long>(1, (total * n_kv + target - 1) / target), hi = max_len;
+      if (lo > hi) lo = hi;
+      while (lo < hi) {
+        const int mid = lo + (hi - lo) / 2;
+        if (fits(mid)) hi = mid;
+        else lo = mid + 1;
+      }
+      rows = std::max(lo, 16);
+    }
+    rows = std::max(rows, (max_len + kMaxSplits - 1) / kMaxSplits);
+    const int rpg_max = large ? 4 : 6;
+    const int r = c->force_rpg ? std::min(c->force_rpg, 6) : std::min(rpg_max, (rows + 15) / 16);
+    a.rpg = r;
+    a.passes = (rows + 16 * r - 1) / (16 * r);
+    if (c->ref_rows <= 0) rows = std::max(16 * r * a.passes, (max_len + kMaxSplits - 1) / kMaxSplits);
+    a.rows_per_split = rows;
+    a.batch = batch;
+    a.split_off[0] = 0;
+    a.max_splits = 1;
+    for (int b = 0; b < batch; ++b) {
+      const int ns = (lens[b] + rows - 1) / rows;
+      a.split_off[b + 1] = a.split_off[b] + ns;
+      a.max_splits = std::max(a.max_splits, ns);
+    }
+    return;
+  }
   if (!large && !c->force_rpg) {
     // Small launches: among the splits of 16 * rpg * passes rows (rpg 1..8)
     // whose workgroups fit one per CU (at most target_wgs, by default the
@@ -581,7 +639,7 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
     for (int p = c->min_passes; p <= p_max; ++p) {
       // No split of p passes beats `best` once its least cost (rpg 1, one
       // split) does not.
-      if (best >= 0 && 35LL * 16 * p + 61LL + 474LL * (p - 1) >= best) break;
+      if (best >= 0 && 35LL * 16 * p + split_cost + 474LL * (p - 1) >= best) break;
       for (int r = 1; r <= 8; ++r) {
         if (!a.merge_inline && (r & (r - 1))) continue;  // two-launch kernels: rpg 1, 2, 4, 8
         const int rows = 16 * r * p;
@@ -593,7 +651,7 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
           splits = std::max(splits, ns);
         }
         if (wgs * n_kv > c->target_wgs) continue;
-        const long long cost = 35LL * rows + 61LL * splits + 474LL * (p - 1);
+        const long long cost = 35LL * rows + split_cost * splits + 474LL * (p - 1);
         if (best < 0 || cost < best) {
           best = cost;
           rpg = r;
@@ -647,8 +705,8 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
     lens[b] = positions[b] + 1;
     a.positions[b] = positions[b];
   }
-  const DecodePlanConfig pc{c->n_cu, c->target_wgs, c->large_wgs, c->force_rpg, c->min_passes,
-                            c->merge_mode};
+  const DecodePlanConfig pc{c->n_cu,       c->target_wgs, c->large_wgs,  c->force_rpg,
+                            c->min_passes, c->merge_mode, c->split_cost, c->ref_rows};
   plan_decode(pc, lens, batch, n_kv, a);
   a.n_kv = n_kv;
   a.group = group;
@@ -665,6 +723,12 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
   a.ws_o = c->ws_o;
   a.ws_ml = c->ws_ml;
   a.counters = c->counters;
+  if (a.merge_ref) {
+    st = ensure_zeroed(reinterpret_cast<unsigned **>(&c->acc), &c->acc_floats,
+                       (size_t)batch * n_kv * kAccStride);
+    if (st) return st;
+    a.acc = c->acc;
+  }
   HIP_TRY(launch_decode(a, s), "decode launch");
   return BNR_OK;
 }
@@ -744,7 +808,9 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
   c->target_wgs = c->n_cu;
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
-  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = atoi(v) != 0;
+  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = std::min(2, std::max(0, atoi(v)));
+  if (const char *v = std::getenv("BNR_DECODE_SPLIT_COST")) c->split_cost = std::max(0, atoi(v));
+  if (const char *v = std::getenv("BNR_DECODE_ROWS")) c->ref_rows = std::max(0, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_PASSES")) c->min_passes = std::min(64, std::max(1, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
@@ -773,6 +839,7 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
       if (p) (void)hipFree(p);
     if (c->ws_ml) (void)hipFree(c->ws_ml);
     if (c->counters) (void)hipFree(c->counters);
+    if (c->acc) (void)hipFree(c->acc);
     if (c->pf_counters) (void)hipFree(c->pf_counters);
     if (c->pf_queue) (void)hipFree(c->pf_queue);
     if (c->stream) (void)hipStreamDestroy(c->stream);

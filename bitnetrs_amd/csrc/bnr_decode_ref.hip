@@ -1,0 +1,434 @@
+// bnr_decode_ref.hip -- gfx950 split-K decode attention with the reference
+// merge (decode_reg_kernel): splits weigh their rows against the score of the
+// newest row and accumulate with device-scope atomics.
+#include "bnr_device.h"
+#include "bnr_internal.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+namespace bnr {
+namespace {
+
+// Device-scope atomic reads.  A read-modify-write always reads the last
+// value of its location's modification order, wherever the lines of that
+// location are cached, so the merge needs no cache maintenance.
+__device__ __forceinline__ float take_f32(float *p) {  // read and clear
+  return __hip_atomic_exchange(p, 0.f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 take_f32x2(float *p) {  // two adjacent floats, read and clear
+  return __builtin_bit_cast(
+      float2, __hip_atomic_exchange(reinterpret_cast<unsigned long long *>(p), 0ull,
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ unsigned long long take_u64(float *p) {
+  return __hip_atomic_exchange(reinterpret_cast<unsigned long long *>(p), 0ull, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float read_rmw(const float *p) {  // read, leave in place
+  return __hip_atomic_fetch_add(const_cast<float *>(p), 0.f, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The last workgroup of (sequence b, kv head h): one batch of atomic
+// exchanges that read the output sums, the weight sums and the masks and
+// leave zeros for the next launch; then the division.  Splits flagged in
+// the masks kept their own maximum and are folded in first.  R: the
+// reference scores; s_L (G floats) and s_mk (4 words): LDS.
+template <int G>
+__device__ __forceinline__ void ref_merge(const DecodeArgs &a, int b, int h, float *acc,
+                                          const float *R, float *s_L, unsigned long long *s_mk,
+                                          int tid, int nthreads) {
+  constexpr int D = kHeadDim;
+  constexpr int NE2 = G * D / 2;  // pairs of outputs
+  float2 o2[(NE2 + 255) / 256];
+#pragma unroll
+  for (int k = 0; k < (NE2 + 255) / 256; ++k) {
+    const int e2 = tid + k * nthreads;
+    if (e2 < NE2) o2[k] = take_f32x2(acc + 2 * e2);
+  }
+  if (tid < G) s_L[tid] = take_f32(acc + kAccL + tid);
+  if (tid >= 64 && tid < 68) s_mk[tid - 64] = take_u64(acc + kAccMask + 2 * (tid - 64));
+  __syncthreads();
+  const bool flagged = (s_mk[0] | s_mk[1] | s_mk[2] | s_mk[3]) != 0;
+#pragma unroll
+  for (int k = 0; k < (NE2 + 255) / 256; ++k) {
+    const int e2 = tid + k * nthreads;
+    if (e2 >= NE2) continue;
+    const int e = 2 * e2, g = e / D;
+    float O[2] = {o2[k].x, o2[k].y};
+    float Ls = s_L[g];
+    if (flagged) {
+      float M = Ls > 0.f ? R[g] : -INFINITY;
+      for (int i = 0; i < 4; ++i) {
+        for (unsigned long long bits = s_mk[i]; bits; bits &= bits - 1) {
+          const long long sp = a.split_off[b] + 64 * i + __builtin_ctzll(bits);
+          const float *ml = reinterpret_cast<const float *>(&a.ws_ml[(sp * a.n_kv + h) * G + g]);
+          const float ms = read_rmw(ml), ls = read_rmw(ml + 1);
+          if (!(ms > -INFINITY)) continue;  // no valid row in that split
+          const float *po = &a.ws_o[(sp * a.n_kv + h) * G * D + e];
+          const float os0 = read_rmw(po), os1 = read_rmw(po + 1);
+          const float mn = fmaxf(M, ms);
+          const float wa = M == -INFINITY ? 0.f : fast_exp2(M - mn), wb = fast_exp2(ms - mn);
+          Ls = Ls * wa + ls * wb;
+          O[0] = O[0] * wa + os0 * wb;
+          O[1] = O[1] * wa + os1 * wb;
+          M = mn;
+        }
+      }
+    }
+    float *op = a.out + b * a.out_bstride + (long long)h * G * D + e;
+    *reinterpret_cast<float2 *>(op) = make_float2(O[0] / Ls, O[1] / Ls);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K decode attention with a reference merge, head_dim 128.
+//
+// Reference merge.  Softmax is invariant to the value subtracted before the
+// exponential, so every split of a (sequence, kv head) weighs its rows by
+// exp2(s - R[g]), where R[g] is the score of row `position` (the newest row)
+// for q head g.  Every workgroup loads that one key row (the raw new key
+// when the append is fused, rotated with the same table entry) and computes
+// R[g] with the same instructions as the row's own score, so all splits use
+// identical references and their unnormalised sums simply add:
+//   out[g] = (sum over splits of O_s[g]) / (sum over splits of l_s[g]).
+// The splits add O_s and l_s into acc with device-scope float atomics (2 KB
+// per split); the last workgroup of the (sequence, kv head), found with a
+// ticket, divides and clears acc for the next launch: the merge loads 2 KB
+// in one round trip instead of every split's partial state, and the
+// per-row-group maxima, weights and rescales of a running-maximum softmax
+// disappear.  The newest row's own weight is exp2(0) = 1, so the sum of
+// weights is at least 1 and cannot underflow.
+//
+// Exact path.  A split whose largest score exceeds R by more than kRefSlack
+// (its weights could overflow) -- or that meets a non-finite score --
+// recomputes its rows with a running maximum per row group, stores that
+// partial state and flags itself in a mask; the merging workgroup folds
+// flagged splits into the reference sums.
+//
+// Rows.  Workgroup = W waves = 4W row groups of 16 lanes.  Lane j of a row
+// group holds dims {4j..4j+3} and {64+4j..64+4j+3} of a row: a dot product
+// is a DPP row sum, and the RoPE pair (i, i+64) of a q/k element sits in one
+// lane.  Row group r takes rows t0 + p*4W*RPG + i*4W + r (pass p, i < RPG);
+// the loads of a pass -- and, for the first pass, of q, the table entry, the
+// reference key and the new value -- are issued as one batch.  The 4W
+// row-group states add through LDS (one reference: plain sums).
+//
+// Summation order across splits follows the order of the atomics, so the
+// last bits of an output can differ between runs (the two older merges of
+// decode_kernel are deterministic).
+// ---------------------------------------------------------------------------
+template <int G, int W, int RPG, bool RAGGED>
+__global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
+  constexpr int D = kHeadDim;
+  constexpr int NRG = 4 * W;  // row groups
+  static_assert(G * D <= kAccL && G <= 4, "accumulator layout holds up to 4 q heads");
+  __shared__ __attribute__((aligned(16))) float s_o[NRG][G][D];
+  __shared__ float s_m[NRG][G], s_l[NRG][G], s_w[NRG][G], s_M[G], s_L[G], s_R[G];
+  __shared__ unsigned long long s_mk[4];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int rg = tid >> 4;
+  const int j = tid & 15;
+  const int b = blockIdx.z;
+  const int s = blockIdx.x;
+  const int nsplit = a.split_off[b + 1] - a.split_off[b];
+  if (RAGGED && s >= nsplit) return;
+  const int h = blockIdx.y;
+  const int pos = a.positions[b];
+  const int L = pos + 1;
+  const int t0 = s * a.rows_per_split;
+  const int t1 = min(t0 + a.rows_per_split, L);
+
+  float *kc = a.k_cache + b * a.cache_bstride + h * a.kv_stride;
+  float *vc = a.v_cache + b * a.cache_bstride + h * a.kv_stride;
+
+  // ---- loads, in use order: q (+cos/sin), the reference key row, the new
+  // value (owner of `position` only), the first pass's K and V rows.
+  const float *qb = a.q + b * a.q_bstride + (long long)h * G * D;
+  float4 qlo[G], qhi[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    qlo[g] = ld4(qb + g * D + 4 * j);
+    qhi[g] = ld4(qb + g * D + 64 + 4 * j);
+  }
+  float4 cs = make_float4(1.f, 1.f, 1.f, 1.f), sn = make_float4(0.f, 0.f, 0.f, 0.f);
+  const bool rope = a.cos_tab != nullptr;
+  if (rope) {
+    cs = ld4(a.cos_tab + (long long)pos * 64 + 4 * j);
+    sn = ld4(a.sin_tab + (long long)pos * 64 + 4 * j);
+  }
+  const bool fused = a.k_new != nullptr;
+  const float *kref = fused ? a.k_new + b * a.kn_bstride + h * D : kc + (long long)pos * D;
+  float4 rklo = ld4(kref + 4 * j), rkhi = ld4(kref + 64 + 4 * j);
+  const bool own_pos = fused && pos >= t0 && pos < t1;
+  float4 nvlo = make_float4(0.f, 0.f, 0.f, 0.f), nvhi = nvlo;
+  if (own_pos) {
+    const float *vn = a.v_new + b * a.kn_bstride + h * D;
+    nvlo = ld4(vn + 4 * j);
+    nvhi = ld4(vn + 64 + 4 * j);
+  }
+  float4 klo[RPG], khi[RPG], vlo[RPG], vhi[RPG];
+  bool valid[RPG];
+  auto load_pass = [&](int tp) {
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const int t = tp + i * NRG + rg;
+      valid[i] = t < t1;
+      const long long off = (long long)(valid[i] ? t : t0) * D;
+      klo[i] = ld4(kc + off + 4 * j);
+      khi[i] = ld4(kc + off + 64 + 4 * j);
+    }
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const long long off = (long long)(valid[i] ? tp + i * NRG + rg : t0) * D;
+      vlo[i] = ld4(vc + off + 4 * j);
+      vhi[i] = ld4(vc + off + 64 + 4 * j);
+    }
+  };
+  load_pass(t0);
+  __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the math
+
+  if (rope) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) rot4(qlo[g], qhi[g], cs, sn, qlo[g], qhi[g]);
+  }
+  if (a.q_rot && s == 0 && rg == 0) {
+    float *qr = a.q_rot + b * a.q_bstride + (long long)h * G * D;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      st4(qr + g * D + 4 * j, qlo[g]);
+      st4(qr + g * D + 64 + 4 * j, qhi[g]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    qlo[g] = scale4(a.scale_log2, qlo[g]);
+    qhi[g] = scale4(a.scale_log2, qhi[g]);
+  }
+  if (fused && rope) {
+    rot4(rklo, rkhi, cs, sn, rklo, rkhi);
+    if (a.k_rot && s == 0 && rg == 0) {
+      float *kr = a.k_rot + b * a.kn_bstride + h * D;
+      st4(kr + 4 * j, rklo);
+      st4(kr + 64 + 4 * j, rkhi);
+    }
+  }
+  // Reference scores: exactly the score row `position` gets below.
+  float R[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) R[g] = row_sum16(dot8(qlo[g], qhi[g], rklo, rkhi));
+
+  // The owner of `position` substitutes the new row -- also where a masked
+  // row past the split's end was clamped onto it: that cache row is not
+  // written yet, and its stale contents would turn the zero weight into
+  // 0 * inf = NaN -- and appends the row.
+  auto put_new = [&](int tp, bool store) {
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+      const int t = tp + i * NRG + rg;
+      if ((valid[i] ? t : t0) == pos) {
+        klo[i] = rklo;
+        khi[i] = rkhi;
+        vlo[i] = nvlo;
+        vhi[i] = nvhi;
+        if (store && valid[i]) {
+          st4(kc + (long long)pos * D + 4 * j, rklo);
+          st4(kc + (long long)pos * D + 64 + 4 * j, rkhi);
+          st4(vc + (long long)pos * D + 4 * j, nvlo);
+          st4(vc + (long long)pos * D + 64 + 4 * j, nvhi);
+        }
+      }
+    }
+  };
+
+  // ---- rows weighed against the reference ----
+  float l[G], mx[G];
+  float4 olo[G], ohi[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    l[g] = 0.f;
+    mx[g] = -INFINITY;
+    olo[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    ohi[g] = olo[g];
+  }
+  for (int tp = t0; tp < t1; tp += NRG * RPG) {
+    if (tp > t0) load_pass(tp);
+    if (own_pos) put_new(tp, true);
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float d = row_sum16(dot8(qlo[g], qhi[g], klo[i], khi[i]));
+        const float sc = valid[i] ? d : -INFINITY;
+        mx[g] = fmaxf(mx[g], sc);
+        const float pr = fast_exp2(sc - R[g]);
+        l[g] += pr;
+        olo[g] = axpy4(pr, vlo[i], olo[g]);
+        ohi[g] = axpy4(pr, vhi[i], ohi[g]);
+      }
+    }
+  }
+  int over = 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    over |= !(mx[g] <= R[g] + kRefSlack) | !(R[g] > -INFINITY && R[g] < INFINITY);
+  const bool exact = __syncthreads_or(over) != 0;
+
+  const int gs = a.split_off[b] + s;  // global split index
+  float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;
+  if (!exact) {
+    // ---- the row groups add through LDS ----
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      st4(&s_o[rg][g][4 * j], olo[g]);
+      st4(&s_o[rg][g][64 + 4 * j], ohi[g]);
+      if (j == 0) s_l[rg][g] = l[g];
+    }
+    __syncthreads();
+    for (int e = tid; e < G * D; e += 64 * W) {
+      const int g = e / D, dim = e % D;
+      float O = s_o[0][g][dim];
+#pragma unroll
+      for (int r = 1; r < NRG; ++r) O += s_o[r][g][dim];
+      if (nsplit == 1) {
+        float Ls = s_l[0][g];
+#pragma unroll
+        for (int r = 1; r < NRG; ++r) Ls += s_l[r][g];
+        a.out[b * a.out_bstride + (long long)h * G * D + e] = O / Ls;
+      } else {
+        add_agent(acc + e, O);
+      }
+    }
+    if (nsplit == 1) return;
+    if (tid < G) {
+      float Ls = s_l[0][tid];
+#pragma unroll
+      for (int r = 1; r < NRG; ++r) Ls += s_l[r][tid];
+      add_agent(acc + kAccL + tid, Ls);
+    }
+  } else {
+    // ---- exact path: the rows again, a running maximum per row group ----
+    float m_run[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m_run[g] = -INFINITY;
+      l[g] = 0.f;
+      olo[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+      ohi[g] = olo[g];
+    }
+    for (int tp = t0; tp < t1; tp += NRG * RPG) {
+      load_pass(tp);
+      if (own_pos) put_new(tp, false);
+#pragma unroll
+      for (int i = 0; i < RPG; ++i) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float d = row_sum16(dot8(qlo[g], qhi[g], klo[i], khi[i]));
+          const float sc = valid[i] ? d : -INFINITY;
+          const float m_new = fmaxf(m_run[g], sc);
+          if (m_new == -INFINITY) continue;  // no valid row yet in this row group
+          const float alpha = fast_exp2(m_run[g] - m_new), pr = fast_exp2(sc - m_new);
+          l[g] = fmaf(l[g], alpha, pr);
+          olo[g] = axpy4(pr, vlo[i], scale4(alpha, olo[g]));
+          ohi[g] = axpy4(pr, vhi[i], scale4(alpha, ohi[g]));
+          m_run[g] = m_new;
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      st4(&s_o[rg][g][4 * j], olo[g]);
+      st4(&s_o[rg][g][64 + 4 * j], ohi[g]);
+      if (j == 0) {
+        s_m[rg][g] = m_run[g];
+        s_l[rg][g] = l[g];
+      }
+    }
+    __syncthreads();
+    if (tid < G) {
+      float M = -INFINITY;
+      for (int r = 0; r < NRG; ++r) M = fmaxf(M, s_m[r][tid]);
+      float Ls = 0.f;
+      for (int r = 0; r < NRG; ++r) {
+        const float wr = M == -INFINITY ? 0.f : fast_exp2(s_m[r][tid] - M);
+        s_w[r][tid] = wr;
+        Ls = fmaf(s_l[r][tid], wr, Ls);
+      }
+      s_M[tid] = M;
+      s_L[tid] = Ls;
+    }
+    __syncthreads();
+    for (int e = tid; e < G * D; e += 64 * W) {
+      const int g = e / D, dim = e % D;
+      float O = 0.f;
+      for (int r = 0; r < NRG; ++r) O = fmaf(s_w[r][g], s_o[r][g][dim], O);
+      if (nsplit == 1)
+        a.out[b * a.out_bstride + (long long)h * G * D + e] = O / s_L[g];
+      else
+        st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], O);
+    }
+    if (nsplit == 1) return;
+    if (tid < G) {
+      float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + tid]);
+      st_agent(ml, s_M[tid]);
+      st_agent(ml + 1, s_L[tid]);
+    }
+    if (tid == 0) {
+      unsigned long long *mask = reinterpret_cast<unsigned long long *>(acc + kAccMask) + (s >> 6);
+      (void)__hip_atomic_fetch_or(mask, 1ull << (s & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  // ---- ticket: the last workgroup of this (sequence, kv head) divides ----
+  // Every wave's device-scope adds and partial stores have completed before
+  // the ticket is taken; the merging workgroup reads them with atomic
+  // read-modify-writes (ref_merge).
+  __builtin_amdgcn_s_waitcnt(0);
+  if (tid < G) s_R[tid] = R[tid];
+  __syncthreads();
+  unsigned *ctr = a.counters + (b * a.n_kv + h) * kCounterStride;
+  if (tid == 0) {
+    const unsigned ticket =
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (ticket == (unsigned)(nsplit - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
+}
+
+template <int G, int W, bool RAGGED>
+hipError_t launch_reg_wr(const DecodeArgs &a, hipStream_t s) {
+  dim3 grid(a.max_splits, a.n_kv, a.batch), block(64 * W);
+  switch (a.rpg) {
+    case 1: decode_reg_kernel<G, W, 1, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 2: decode_reg_kernel<G, W, 2, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 3: decode_reg_kernel<G, W, 3, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 4: decode_reg_kernel<G, W, 4, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 5: decode_reg_kernel<G, W, 5, RAGGED><<<grid, block, 0, s>>>(a); break;
+    case 6: decode_reg_kernel<G, W, 6, RAGGED><<<grid, block, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s) {
+  if (!a.acc) return hipErrorInvalidValue;
+  bool ragged = false;
+  for (int b = 0; b < a.batch; ++b)
+    ragged |= (a.split_off[b + 1] - a.split_off[b]) != a.max_splits;
+  switch (a.group) {
+    case 1: return ragged ? launch_reg_wr<1, 4, true>(a, s) : launch_reg_wr<1, 4, false>(a, s);
+    case 2: return ragged ? launch_reg_wr<2, 4, true>(a, s) : launch_reg_wr<2, 4, false>(a, s);
+    case 4: return ragged ? launch_reg_wr<4, 4, true>(a, s) : launch_reg_wr<4, 4, false>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bnr

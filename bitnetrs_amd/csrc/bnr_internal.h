@@ -18,6 +18,18 @@ constexpr int kMaxBatchPerLaunch = 64;
 constexpr int kMaxSplits = 256;
 // Ticket counters are 256 bytes apart: atomics on one cache line serialise.
 constexpr int kCounterStride = 64;
+// Reference merge accumulators of one (sequence, kv head), in floats: the
+// G*128 output sums at 0, the G weight sums at kAccL, four 64-bit masks of
+// splits that took the exact path at kAccMask (G <= 4).
+constexpr int kAccL = 512;
+constexpr int kAccMask = 576;
+constexpr int kAccStride = 640;
+// A split whose largest score exceeds the reference by more than this (in
+// log2 units) would overflow the reference-weighted sums: it takes the
+// exact path (own running maximum, partial state for the merging
+// workgroup).  Weights of at most 2^64 keep 65536 rows of |v| <= 2^40
+// below FLT_MAX (2^128).
+constexpr float kRefSlack = 64.0f;
 
 // RoPE + append over n_tokens consecutive positions of one sequence.  q and
 // k are rotated in place; when k_cache is non-null the rotated k rows and the
@@ -55,11 +67,21 @@ struct DecodeArgs {
   int rpg;                        // rows per 16-lane row group and pass
   int passes;
   int merge_inline;                // 1: last-workgroup merge; 0: second kernel
+  // Reference merge (merge_ref = 1, decode_ref_kernel): every split weighs
+  // its rows against one reference score per q head -- the score of row
+  // `position`, which every workgroup computes identically -- and adds its
+  // unnormalised sums into acc with device-scope float atomics; the last
+  // workgroup of a (sequence, kv head) divides.  acc: [batch][n_kv] x
+  // kAccStride floats, zero between launches.
+  int merge_ref;
+  float *acc;
   int max_splits;                  // largest split count of the launch (grid x)
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
 };
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
+// The reference-merge kernel alone (a.merge_ref; group 1, 2 or 4).
+hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s);
 
 // Decode planner inputs: the device and the context's tuning state.
 struct DecodePlanConfig {
@@ -68,7 +90,9 @@ struct DecodePlanConfig {
   int large_wgs;   // launches of at least this many 64-row workgroups use the two-launch merge
   int force_rpg;   // 0, or a fixed rows-per-row-group (tuning)
   int min_passes;  // at least this many passes per split (tuning, default 1)
-  int merge_mode;  // -1: planner decides; 0: second kernel; 1: in-kernel
+  int merge_mode;  // -1: reference merge (default); 0: second kernel; 1: in-kernel ticket; 2: reference merge
+  int split_cost;  // planner cost of one split of the in-kernel merges (ns), -1: the mode's default
+  int ref_rows;    // reference merge: rows per split (0: planner decides)
 };
 // Split-K plan of one decode launch over sequences of lens[b] rows: fills
 // a.rpg, a.passes, a.rows_per_split, a.batch, a.split_off, a.max_splits and

@@ -1,9 +1,10 @@
 """The split-K decode planner (bnr::plan_decode): split sizes and counts
-consistent with the rows, the two-launch merge only where its kernels exist,
-small launches within one workgroup per CU and at the cheapest split by the
-planner's time estimate, and the plans of the 2B shape at the fitted
-contexts.  A host-only harness is built with hipcc against the library and
-run over 5400 seeded launches (no GPU needed)."""
+consistent with the rows; for the reference merge (default) the smallest
+split whose workgroups fit the launch's target; for the forced ticket and
+two-launch merges the two-launch merge only where its kernels exist and
+small launches at the cheapest split by the planner's time estimate; the
+plans of the 2B shape.  A host-only harness is built with hipcc against the
+library and run over 9000 seeded launches (no GPU needed)."""
 import os
 import shutil
 import subprocess
