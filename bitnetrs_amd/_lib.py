@@ -94,6 +94,8 @@ SIGNATURES = {
                                        _vp, _vp, _sz, _vp]),
     "bnr_dev_decode_attention": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
                                             _vp]),
+    "bnr_dev_decode_attention_noalloc": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz,
+                                                    _sz, _vp]),
     "bnr_dev_decode_step": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _c.c_float, _vp,
                                        _vp, _sz, _vp, _vp, _vp, _vp]),
     "bnr_dev_decode_step_batched": (_c.c_int, [_vp, _vp, _vp, _vp, _i32p, _sz, _sz, _sz, _sz,

@@ -165,6 +165,15 @@ class HipBackend:
             self._h, _dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
             _dev(out, "out"), n_heads, n_kv_heads, head_dim, cur_pos, _stream(stream)))
 
+    def dev_decode_attention_noalloc(self, q, k_cache, v_cache, cap, out, n_heads, n_kv_heads,
+                                     head_dim, cur_pos, stream=None) -> None:
+        """dev_decode_attention without any device allocation (the merge state
+        lives in the library's per-GPU device array); overlapping calls on one
+        GPU race."""
+        _lib.check(self._L.bnr_dev_decode_attention_noalloc(
+            self._h, _dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
+            _dev(out, "out"), n_heads, n_kv_heads, head_dim, cur_pos, _stream(stream)))
+
     def dev_decode_step(self, q, k, v, position, n_heads, n_kv_heads, head_dim, theta, k_cache,
                         v_cache, cap, out, q_rot=None, k_rot=None, stream=None) -> None:
         _lib.check(self._L.bnr_dev_decode_step(

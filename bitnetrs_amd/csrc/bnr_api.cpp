@@ -212,6 +212,10 @@ struct bnr_ctx {
   int split_cost = -1;  // planner cost of a split of the in-kernel merges (ns); -1: mode default
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
 
+  // device scratch of bnr_dev_decode_attention_noalloc (this GPU's copy)
+  void *noalloc = nullptr;
+  std::string noalloc_err;
+
   // prefill planner
   int n_cu = 256;
   int pf_chunk_tiles = -1;  // -1: planner decides; else key tiles per chunk
@@ -806,6 +810,13 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
     return err_hip(e, "hipStreamCreate");
   }
   if (prop.multiProcessorCount > 0) c->n_cu = prop.multiProcessorCount;
+  // The allocation-free entry point's scratch: resolved (and its merge state
+  // zeroed) once per device; a failure here only disables that entry point.
+  e = noalloc_scratch(device_id, c->stream, &c->noalloc);
+  if (e != hipSuccess) {
+    c->noalloc = nullptr;
+    c->noalloc_err = std::string("no-alloc scratch setup failed: ") + hipGetErrorString(e);
+  }
   c->target_wgs = c->n_cu;
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = std::min(2, std::max(0, atoi(v)));
@@ -1295,6 +1306,54 @@ extern "C" int bnr_dev_decode_attention(bnr_ctx *c, const float *q, const float 
     st = run_generic(c, q, k_cache, v_cache, kv_stride, out, n_heads, n_kv_heads, head_dim, cur_pos, s);
   }
   return st ? st : set_ok();
+}
+
+extern "C" int bnr_dev_decode_attention_noalloc(bnr_ctx *c, const float *q, const float *k_cache,
+                                                const float *v_cache, size_t cap, float *out,
+                                                size_t n_heads, size_t n_kv_heads,
+                                                size_t head_dim, size_t cur_pos, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rows(cur_pos, cap);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !out) return err_backend("decode_attention_noalloc: NULL pointer");
+  if (!fast_shape(n_heads, n_kv_heads, head_dim))
+    return err_config(fmt("decode_attention_noalloc needs head_dim %d and n_heads/n_kv_heads in "
+                          "{1,2,4}, got head_dim %zu, n_heads %zu, n_kv_heads %zu",
+                          kHeadDim, head_dim, n_heads, n_kv_heads));
+  if (n_heads > (size_t)kNoAllocMaxHeads)
+    return err_config(fmt("decode_attention_noalloc holds at most %d query heads, got %zu",
+                          kNoAllocMaxHeads, n_heads));
+  if (!(aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out)))
+    return err_shape("16-byte aligned device pointers", "an unaligned pointer");
+  if (cur_pos >= (size_t)INT32_MAX)
+    return err_shape(fmt("cur_pos < %d", INT32_MAX), fmt("cur_pos = %zu", cur_pos));
+  std::lock_guard<std::mutex> lk(c->mu);
+  if (!c->noalloc) return err_backend(c->noalloc_err.empty() ? "no-alloc scratch unavailable" : c->noalloc_err);
+  DeviceGuard dg(c->device);
+  DecodeArgs a{};
+  a.q = q;
+  a.k_cache = const_cast<float *>(k_cache);
+  a.v_cache = const_cast<float *>(v_cache);
+  a.kv_stride = (long long)(cap * head_dim);
+  a.out = out;
+  const int lens[1] = {(int)cur_pos + 1};
+  a.positions[0] = (int)cur_pos;
+  // Always the reference merge: its state fits the scratch for any context.
+  const DecodePlanConfig pc{c->n_cu, c->target_wgs, c->large_wgs, c->force_rpg, c->min_passes,
+                            2,       c->split_cost, c->ref_rows};
+  plan_decode(pc, lens, 1, (int)n_kv_heads, a);
+  if (a.max_splits > kMaxSplits) return err_backend("decode_attention_noalloc: too many splits");
+  a.n_kv = (int)n_kv_heads;
+  a.group = (int)(n_heads / n_kv_heads);
+  a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
+  char *base = static_cast<char *>(c->noalloc);
+  a.acc = reinterpret_cast<float *>(base);
+  a.counters = reinterpret_cast<unsigned *>(base + kNoAllocAccBytes);
+  a.ws_ml = reinterpret_cast<float2 *>(base + kNoAllocZeroBytes);
+  a.ws_o = reinterpret_cast<float *>(base + kNoAllocZeroBytes + kNoAllocMlBytes);
+  HIP_TRY(launch_decode(a, (hipStream_t)stream), "decode launch");
+  return set_ok();
 }
 
 namespace {

@@ -83,6 +83,21 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 // The reference-merge kernel alone (a.merge_ref; group 1, 2 or 4).
 hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s);
 
+// Scratch of the allocation-free decode entry point (bnr_noalloc.hip), for
+// at most kNoAllocMaxHeads query heads and kMaxSplits splits: the
+// reference-merge accumulators and tickets (zero between launches), then the
+// exact path's partial states.  About 4.15 MiB per GPU.
+constexpr int kNoAllocMaxHeads = 32;
+constexpr long long kNoAllocAccBytes = (long long)kNoAllocMaxHeads * kAccStride * 4;
+constexpr long long kNoAllocCounterBytes = (long long)kNoAllocMaxHeads * kCounterStride * 4;
+constexpr long long kNoAllocZeroBytes = kNoAllocAccBytes + kNoAllocCounterBytes;
+constexpr long long kNoAllocMlBytes = (long long)kMaxSplits * kNoAllocMaxHeads * 8;
+constexpr long long kNoAllocOBytes = (long long)kMaxSplits * kNoAllocMaxHeads * kHeadDim * 4;
+constexpr long long kNoAllocScratchBytes = kNoAllocZeroBytes + kNoAllocMlBytes + kNoAllocOBytes;
+// The scratch's address on `device` (current), set up once per device: its
+// merge state zeroed by a kernel on `s`, then `s` synchronised.
+hipError_t noalloc_scratch(int device, hipStream_t s, void **out);
+
 // Decode planner inputs: the device and the context's tuning state.
 struct DecodePlanConfig {
   int n_cu;        // CUs of the device

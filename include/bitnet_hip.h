@@ -143,6 +143,21 @@ int bnr_dev_decode_attention(bnr_ctx *ctx, const float *q, const float *k_cache,
                              size_t n_kv_heads, size_t head_dim, size_t cur_pos,
                              void *stream);
 
+/* bnr_dev_decode_attention that allocates nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * split-K merge state lives in a device array of the library (about 4.15
+ * MiB, one copy per GPU, set up by bnr_create); calls never allocate, free
+ * or synchronise.  Limits: head_dim 128, n_heads / n_kv_heads in {1, 2, 4},
+ * n_heads <= 32, 16-byte aligned pointers; anything else is
+ * BNR_INVALID_CONFIG / BNR_INVALID_SHAPE.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other
+ * contexts, other threads) race and must be serialised by the caller. */
+int bnr_dev_decode_attention_noalloc(bnr_ctx *ctx, const float *q, const float *k_cache,
+                                     const float *v_cache, size_t cap, float *out,
+                                     size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                                     size_t cur_pos, void *stream);
+
 /* One fused decode step of one layer, in a single kernel launch: rotate q
  * (raw, [n_heads x d]) and k (raw, [n_kv_heads x d]) at `position`, append
  * the rotated k row and the v row at `position`, and attend over rows
