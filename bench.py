@@ -19,6 +19,7 @@ threads) timed on a bounded sample of the same workload on this host.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -122,6 +123,7 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: 
     # event-pair figure (spin-held queue) is reported beside it.
     kernel_ms = ms_step if graph is not None else per_launch_ms(torch, step, min(steps, 200))
     pair_ms = per_launch_ms(torch, step, min(steps, 200))
+    floor_ms = stream_floor_ms(torch, be, kc, vc, steps)
     nbytes = decode_bytes(L)
     res = {
         "ms_per_step": ms_step,
@@ -130,6 +132,7 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: 
         "pair_ms": pair_ms,
         "kernel_gbs": nbytes / (kernel_ms * 1e-3) / 1e9,
         "bytes_per_step": nbytes,
+        "floor_ms": floor_ms,
         "graph": graph is not None,
         "host": {"q": q[0].cpu().numpy(), "k": k[0].cpu().numpy(), "v": v[0].cpu().numpy(),
                  "k_cache": kc[0].cpu().numpy(), "v_cache": vc[0].cpu().numpy()},
@@ -137,6 +140,107 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: 
     del kc, vc
     torch.cuda.empty_cache()
     return res
+
+
+def stream_floor_ms(torch, be, kc, vc, steps: int) -> float:
+    """A plain streaming read of the same rotated K and V caches (one layer's
+    21 MB per launch, the layers round-robin as in the decode timing), timed
+    the same way: what one launch of that many bytes can reach on this part."""
+    n_layers = kc.shape[0]
+
+    def read(i):
+        r = i % n_layers
+        be.dev_stream_read(kc[r], vc[r])
+
+    for i in range(20):
+        read(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            read(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / steps
+
+
+def bench_trait_path(be, steps: int = 300, pos_end: int = 4095):
+    """The path an unchanged bitnet-inference drives (bitnet-model/src/lib.rs:
+    1004-1036): per token and layer, Backend::rope_embed on host q/k slices,
+    store_kv into the host KVCache, Backend::masked_attention over the host
+    caches -- here through the C ABI's host-slice entry points, timed at
+    positions pos_end-steps+1 .. pos_end after 10 untimed ones (the HBM
+    mirror takes one new row per call).
+    Also one rms_norm and one sqrelu_gate host call of the 2B shape."""
+    import numpy as np
+
+    rng = np.random.default_rng(0xB17E7090)
+    cap = 4096
+    kc = rng.standard_normal((HKV, cap, D), dtype=np.float32)
+    vc = rng.standard_normal((HKV, cap, D), dtype=np.float32)
+    q0 = rng.standard_normal(HQ * D, dtype=np.float32)
+    k0 = rng.standard_normal(HKV * D, dtype=np.float32)
+    v0 = rng.standard_normal(HKV * D, dtype=np.float32)
+    out = np.zeros(HQ * D, np.float32)
+    kcf, vcf = kc.reshape(-1), vc.reshape(-1)
+    warm = 10
+    p0 = pos_end - steps + 1
+    be.mirror_invalidate()
+    # first call syncs the mirror (rows 0..p0-warm-1 uploaded once), then
+    # `warm` positions untimed (first-use staging allocations)
+    q, k = q0.copy(), k0.copy()
+    be.rope_embed(q, k, p0 - warm - 1, D, HQ, HKV, THETA)
+    be.masked_attention(q, kcf, vcf, out, HQ, HKV, D, p0 - warm - 1)
+    t_rope = t_attn = 0.0
+    # The library is an FFI boundary (the reference's caller is Rust): Python's
+    # cyclic garbage collector, whose full passes take tens of ms in a process
+    # holding torch, stays off while the calls are timed.
+    gc.collect()
+    gc.disable()
+    for pos in range(p0 - warm, pos_end + 1):
+        q, k = q0.copy(), k0.copy()
+        t0 = time.perf_counter()
+        be.rope_embed(q, k, pos, D, HQ, HKV, THETA)
+        t1 = time.perf_counter()
+        kc[:, pos] = k.reshape(HKV, D)
+        vc[:, pos] = v0.reshape(HKV, D)
+        t2 = time.perf_counter()
+        be.masked_attention(q, kcf, vcf, out, HQ, HKV, D, pos)
+        t3 = time.perf_counter()
+        if pos >= p0:
+            t_rope += t1 - t0
+            t_attn += t3 - t2
+    gc.enable()
+    hidden, ffn = 2560, 6912
+    x = rng.standard_normal(hidden, dtype=np.float32)
+    g = rng.uniform(0.8, 1.2, hidden).astype(np.float32)
+    y = np.zeros(hidden, np.float32)
+    gate = rng.standard_normal(ffn, dtype=np.float32)
+    up = rng.standard_normal(ffn, dtype=np.float32)
+    inner = np.zeros(ffn, np.float32)
+    n_glue = 200
+    for _ in range(5):
+        be.rms_norm(x, g, 1e-5, y)
+        be.sqrelu_gate(gate, up, inner)
+    gc.collect()
+    gc.disable()
+    t0 = time.perf_counter()
+    for _ in range(n_glue):
+        be.rms_norm(x, g, 1e-5, y)
+    t1 = time.perf_counter()
+    for _ in range(n_glue):
+        be.sqrelu_gate(gate, up, inner)
+    t2 = time.perf_counter()
+    gc.enable()
+    return {"rope_us": t_rope / steps * 1e6, "attn_us": t_attn / steps * 1e6,
+            "token_layer_us": (t_rope + t_attn) / steps * 1e6, "steps": steps,
+            "rms_norm_us": (t1 - t0) / n_glue * 1e6, "sqrelu_gate_us": (t2 - t1) / n_glue * 1e6}
 
 
 def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048, n_layers: int = 4):
@@ -594,6 +698,8 @@ def main() -> int:
     ap.add_argument("--no-gemv", action="store_true", help="skip the ternary GEMV workload")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the i8 LM head workload")
     ap.add_argument("--no-model", action="store_true", help="skip the whole-model decode token")
+    ap.add_argument("--no-trait", action="store_true",
+                    help="skip the host-slice (Backend trait) path timing")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds per CPU baseline")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a captured graph")
@@ -640,10 +746,26 @@ def main() -> int:
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("decode_kernel", {}).get("bytes_per_launch"),
-                     "kernel": "decode_kernel", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
+                     "kernel": "decode_reg_kernel", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
                      "event_pair_us": round(dec["pair_ms"] * 1e3, 3),
-                     "bytes_per_launch": dec["bytes_per_step"]},
+                     "bytes_per_launch": dec["bytes_per_step"],
+                     "stream_floor_us": round(dec["floor_ms"] * 1e3, 3),
+                     "stream_floor_gbs": round(dec["bytes_per_step"] / (dec["floor_ms"] * 1e-3) / 1e9, 1),
+                     "frac_of_stream_floor": round(dec["floor_ms"] / dec["kernel_ms"], 4)},
     }
+    if not args.no_trait:
+        tp = bench_trait_path(be)
+        log(f"trait path at pos 4095: rope_embed {tp['rope_us']:.1f} us + masked_attention "
+            f"{tp['attn_us']:.1f} us = {tp['token_layer_us']:.1f} us per token and layer; "
+            f"rms_norm {tp['rms_norm_us']:.1f} us, sqrelu_gate {tp['sqrelu_gate_us']:.1f} us")
+        line["trait_path"] = {
+            "workload": "host_slice_rope_embed_masked_attention_pos4095_hq20_hkv5_d128_fp32",
+            "us_per_token_layer": round(tp["token_layer_us"], 2),
+            "rope_embed_us": round(tp["rope_us"], 2), "masked_attention_us": round(tp["attn_us"], 2),
+            "rms_norm_host_us": round(tp["rms_norm_us"], 2),
+            "sqrelu_gate_host_us": round(tp["sqrelu_gate_us"], 2),
+            "timed": f"{tp['steps']} consecutive positions after 10 untimed, wall clock per "
+                     "host call (PCIe included), Python GC off"}
     if not args.no_prefill:
         pre = bench_prefill(torch, be, args.prefill_steps, 2)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, {pre['tflops']:.2f} TFLOP/s; attention "
@@ -726,6 +848,10 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)
+        if "trait_path" in line:
+            cb = line["cpu_baseline"]
+            line["trait_path"]["cpu_oracle_us_per_token_layer"] = round(
+                decode_bytes(4096) / (cb["value"] * 1e9) * 1e6, 2)
         if not args.no_prefill:
             line["prefill"]["cpu_baseline"] = cpu_baseline_prefill(args.cpu_budget)
         if not args.no_gemv:

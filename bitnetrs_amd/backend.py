@@ -165,6 +165,11 @@ class HipBackend:
             self._h, _dev(q, "q"), _dev(k_cache, "k_cache"), _dev(v_cache, "v_cache"), cap,
             _dev(out, "out"), n_heads, n_kv_heads, head_dim, cur_pos, _stream(stream)))
 
+    def dev_stream_read(self, a, b, stream=None) -> None:
+        """Plain streaming read of two float32 CUDA tensors (measurement)."""
+        _lib.check(self._L.bnr_dev_stream_read(self._h, _dev(a, "a"), a.numel() * 4, _dev(b, "b"),
+                                               b.numel() * 4, _stream(stream)))
+
     def dev_decode_attention_noalloc(self, q, k_cache, v_cache, cap, out, n_heads, n_kv_heads,
                                      head_dim, cur_pos, stream=None) -> None:
         """dev_decode_attention without any device allocation (the merge state

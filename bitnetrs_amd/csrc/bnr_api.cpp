@@ -158,6 +158,25 @@ struct DeviceGuard {
 
 constexpr size_t kMaxMirrors = 256;
 
+// Merge state of split-K decode launches: split partials (exact path),
+// tickets and reference-merge accumulators.  Kernels leave tickets and
+// accumulators at zero after every launch; launches that share a workspace
+// must be ordered (one stream, or synchronised).
+struct DecodeWs {
+  float *ws_o = nullptr;
+  size_t ws_o_floats = 0;
+  float2 *ws_ml = nullptr;
+  size_t ws_ml_n = 0;
+  unsigned *counters = nullptr;
+  size_t n_counters = 0;
+  float *acc = nullptr;  // reference-merge accumulators
+  size_t acc_floats = 0;
+  float *scores = nullptr;  // generic kernel: scores of every row
+  size_t scores_floats = 0;
+  float *rot = nullptr;  // other shapes: rotated copies of q and k
+  size_t rot_floats = 0;
+};
+
 }  // namespace
 
 struct bnr_ctx {
@@ -172,17 +191,10 @@ struct bnr_ctx {
   float tab_theta = 0.f;
   float *d_cos = nullptr, *d_sin = nullptr;
 
-  // workspace
-  float *ws_o = nullptr;
-  size_t ws_o_floats = 0;
-  float2 *ws_ml = nullptr;
-  size_t ws_ml_n = 0;
-  unsigned *counters = nullptr;
-  size_t n_counters = 0;
-  float *acc = nullptr;  // reference-merge accumulators (zero between launches)
-  size_t acc_floats = 0;
-  float *scratch = nullptr;  // generic-kernel scores and host-path staging
-  size_t scratch_floats = 0;
+  // Split-K decode workspaces: one for launches on the library's own stream
+  // (the host-slice entry points), one for launches on callers' streams (the
+  // device entry points), so that the two kinds never share merge state.
+  DecodeWs hws, dws;
   float *pf_ws = nullptr;  // prefill chunk partials
   size_t pf_ws_floats = 0;
   unsigned *pf_counters = nullptr;
@@ -191,10 +203,13 @@ struct bnr_ctx {
   size_t n_pf_queue = 0;
 
   // host-path staging
-  float *d_q = nullptr, *d_k = nullptr, *d_out = nullptr;
-  size_t d_q_n = 0, d_k_n = 0, d_out_n = 0;
+  float *d_q = nullptr, *d_out = nullptr;
+  size_t d_q_n = 0, d_out_n = 0;
   float *h_stage = nullptr;  // pinned host staging of the host-slice calls
   size_t h_stage_n = 0;
+  float *h_zc = nullptr;  // zero-copy staging: pinned host memory kernels read and write
+  float *d_zc = nullptr;  // its device address
+  size_t h_zc_n = 0;
 
   // mirrors, most recently used first
   std::list<Mirror> mirrors;
@@ -211,6 +226,7 @@ struct bnr_ctx {
   int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel ticket; 2: reference merge
   int split_cost = -1;  // planner cost of a split of the in-kernel merges (ns); -1: mode default
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
+  int ref_waves = 8;    // reference merge: waves per workgroup of small launches (4 or 8)
 
   // device scratch of bnr_dev_decode_attention_noalloc (this GPU's copy)
   void *noalloc = nullptr;
@@ -298,6 +314,41 @@ int get_host(bnr_ctx *c, void *host, const void *dev, size_t bytes, const char *
   return BNR_OK;
 }
 
+// Grow-only zero-copy staging: pinned, non-coherent host memory mapped into
+// the device's address space.  The kernels of the per-token host-slice
+// entry points read their inputs from it and write their outputs into it,
+// so such a call issues no copy commands.  Non-coherent host memory is
+// coherent at kernel boundaries: the host fills it before the launch and
+// reads it after host_wait.
+int ensure_zc(bnr_ctx *c, size_t n) {
+  if (c->h_zc_n >= n && c->h_zc) return BNR_OK;
+  if (c->h_zc) {
+    (void)hipStreamSynchronize(c->stream);
+    (void)hipHostFree(c->h_zc);
+    c->h_zc = c->d_zc = nullptr;
+    c->h_zc_n = 0;
+  }
+  const size_t want = std::max<size_t>(n, 65536);
+  HIP_TRY(hipHostMalloc((void **)&c->h_zc, want * sizeof(float),
+                        hipHostMallocMapped | hipHostMallocNonCoherent),
+          "zero-copy staging alloc");
+  hipError_t e = hipHostGetDevicePointer((void **)&c->d_zc, c->h_zc, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(c->h_zc);
+    c->h_zc = c->d_zc = nullptr;
+    return err_hip(e, "zero-copy staging map");
+  }
+  c->h_zc_n = want;
+  return BNR_OK;
+}
+
+// Waits for the library's stream: a host-slice call returns with its
+// outputs written.
+int host_wait(bnr_ctx *c, const char *what) {
+  HIP_TRY(hipStreamSynchronize(c->stream), what);
+  return BNR_OK;
+}
+
 // Grow-only, zero-filled ticket counters (kernels leave them zero).
 int ensure_zeroed(unsigned **p, size_t *cap, size_t n) {
   if (*cap >= n && *p) return BNR_OK;
@@ -315,23 +366,35 @@ int ensure_zeroed(unsigned **p, size_t *cap, size_t n) {
   return BNR_OK;
 }
 
-int ensure_counters(bnr_ctx *c, size_t n) { return ensure_zeroed(&c->counters, &c->n_counters, n); }
-
-int ensure_ws(bnr_ctx *c, size_t o_floats, size_t ml_n) {
-  int st = ensure_buf(&c->ws_o, &c->ws_o_floats, o_floats, "workspace alloc");
+int ensure_ws(DecodeWs &w, size_t o_floats, size_t ml_n) {
+  int st = ensure_buf(&w.ws_o, &w.ws_o_floats, o_floats, "workspace alloc");
   if (st) return st;
-  if (c->ws_ml_n < ml_n || !c->ws_ml) {
-    if (c->ws_ml) {
+  if (w.ws_ml_n < ml_n || !w.ws_ml) {
+    if (w.ws_ml) {
       (void)hipDeviceSynchronize();
-      (void)hipFree(c->ws_ml);
-      c->ws_ml = nullptr;
+      (void)hipFree(w.ws_ml);
+      w.ws_ml = nullptr;
     }
     size_t want = std::max<size_t>(ml_n, 1024);
-    HIP_TRY(hipMalloc((void **)&c->ws_ml, want * sizeof(float2)), "workspace alloc");
-    c->ws_ml_n = want;
+    HIP_TRY(hipMalloc((void **)&w.ws_ml, want * sizeof(float2)), "workspace alloc");
+    w.ws_ml_n = want;
   }
   return BNR_OK;
 }
+
+void free_ws(DecodeWs &w) {
+  if (w.ws_o) (void)hipFree(w.ws_o);
+  if (w.ws_ml) (void)hipFree(w.ws_ml);
+  if (w.counters) (void)hipFree(w.counters);
+  if (w.acc) (void)hipFree(w.acc);
+  if (w.scores) (void)hipFree(w.scores);
+  if (w.rot) (void)hipFree(w.rot);
+  w = DecodeWs{};
+}
+
+// The workspace of launches on stream s: the host-slice entry points run on
+// the library's own stream, the device entry points on the caller's.
+DecodeWs &ws_for(bnr_ctx *c, hipStream_t s) { return s == c->stream ? c->hws : c->dws; }
 
 // Prefill key-range chunking.  The planner replays the launch's dispatch for
 // each candidate chunk size and keeps the shortest span.  Workgroups go to
@@ -466,6 +529,7 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
 // faster at 6 tiles than at 4, 512 queries after 1536 cached 14 % faster at
 // 10 than at 4 or 16).
 constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
+constexpr long long kPrefillMaxSplitItems = 8192;  // (kv head, item) pairs of a planned split
 
 int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
   for (const PrefillPlanEntry &e : c->pf_plans)
@@ -473,7 +537,8 @@ int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
   int best = kPrefillNoSplit;
   double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, c->n_cu);
   for (int ct : kPrefillChunkCandidates) {
-    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > 8192) continue;
+    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > kPrefillMaxSplitItems)
+      continue;
     const double span = prefill_span(n_tokens, start_pos, n_kv, ct, c->n_cu);
     if (span < best_span * 0.99) {
       best_span = span;
@@ -582,7 +647,7 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
     // target: one round of one workgroup per CU (target_wgs) for a small
     // launch, eight workgroups per CU (two resident at rpg 4) for a large
     // one.  A split is a contiguous range of rows of one (sequence, kv head)
-    // in passes of 16 * rpg rows (rpg up to 6; 4 for large launches).
+    // in passes of 4 * waves * rpg rows.
     const long long target = large ? 8LL * c->target_wgs : c->target_wgs;
     int max_len = 1;
     long long total = 0;
@@ -609,11 +674,16 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
       rows = std::max(lo, 16);
     }
     rows = std::max(rows, (max_len + kMaxSplits - 1) / kMaxSplits);
-    const int rpg_max = large ? 4 : 6;
-    const int r = c->force_rpg ? std::min(c->force_rpg, 6) : std::min(rpg_max, (rows + 15) / 16);
+    // Small launches run 8-wave workgroups (one per CU) with up to 3 rows
+    // per row group and pass; large ones 4-wave workgroups (two resident per
+    // CU) with up to 4 (graph-timed sweeps on MI355X, contexts 512-32768).
+    a.ref_waves = large || c->ref_waves == 4 ? 4 : 8;
+    const int nrg = 4 * a.ref_waves;  // row groups of 16 lanes
+    const int rpg_max = large ? 4 : a.ref_waves == 8 ? 3 : 6;
+    const int r = c->force_rpg ? std::min(c->force_rpg, 6) : std::min(rpg_max, (rows + nrg - 1) / nrg);
     a.rpg = r;
-    a.passes = (rows + 16 * r - 1) / (16 * r);
-    if (c->ref_rows <= 0) rows = std::max(16 * r * a.passes, (max_len + kMaxSplits - 1) / kMaxSplits);
+    a.passes = (rows + nrg * r - 1) / (nrg * r);
+    if (c->ref_rows <= 0) rows = std::max(nrg * r * a.passes, (max_len + kMaxSplits - 1) / kMaxSplits);
     a.rows_per_split = rows;
     a.batch = batch;
     a.split_off[0] = 0;
@@ -710,28 +780,31 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
     a.positions[b] = positions[b];
   }
   const DecodePlanConfig pc{c->n_cu,       c->target_wgs, c->large_wgs,  c->force_rpg,
-                            c->min_passes, c->merge_mode, c->split_cost, c->ref_rows};
+                            c->min_passes, c->merge_mode, c->split_cost, c->ref_rows,
+                            c->ref_waves};
   plan_decode(pc, lens, batch, n_kv, a);
   a.n_kv = n_kv;
   a.group = group;
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
   // Size the workspace for the most splits any position below `cap` can
-  // need, so that later calls on the same caches -- including calls under
-  // HIP graph capture -- never allocate.
+  // need, and tickets and accumulators for the largest batch of a launch,
+  // so that later calls on the same caches -- including calls under HIP
+  // graph capture -- never allocate.
+  DecodeWs &w = ws_for(c, s);
   const size_t worst = std::min<size_t>(kMaxSplits, (cap + 15) / 16);
   const size_t splits = std::max<size_t>((size_t)a.split_off[batch], worst * (size_t)batch);
-  int st = ensure_ws(c, splits * n_kv * group * kHeadDim, splits * n_kv * group);
+  int st = ensure_ws(w, splits * n_kv * group * kHeadDim, splits * n_kv * group);
   if (st) return st;
-  st = ensure_counters(c, (size_t)batch * n_kv * kCounterStride);
+  const size_t heads = (size_t)std::max(batch, kMaxBatchPerLaunch) * n_kv;
+  st = ensure_zeroed(&w.counters, &w.n_counters, heads * kCounterStride);
   if (st) return st;
-  a.ws_o = c->ws_o;
-  a.ws_ml = c->ws_ml;
-  a.counters = c->counters;
+  a.ws_o = w.ws_o;
+  a.ws_ml = w.ws_ml;
+  a.counters = w.counters;
   if (a.merge_ref) {
-    st = ensure_zeroed(reinterpret_cast<unsigned **>(&c->acc), &c->acc_floats,
-                       (size_t)batch * n_kv * kAccStride);
+    st = ensure_zeroed(reinterpret_cast<unsigned **>(&w.acc), &w.acc_floats, heads * kAccStride);
     if (st) return st;
-    a.acc = c->acc;
+    a.acc = w.acc;
   }
   HIP_TRY(launch_decode(a, s), "decode launch");
   return BNR_OK;
@@ -741,7 +814,11 @@ int run_generic(bnr_ctx *c, const float *dq, const float *dk, const float *dv, l
                 float *dout, size_t n_heads, size_t n_kv, size_t head_dim, size_t cur_pos,
                 hipStream_t s) {
   const size_t L = cur_pos + 1;
-  int st = ensure_buf(&c->scratch, &c->scratch_floats, n_heads * L, "scratch alloc");
+  // scores for every row of the cache (kv_stride / head_dim rows): later
+  // calls on it never allocate
+  const size_t rows = std::max(L, (size_t)kv_stride / head_dim);
+  DecodeWs &w = ws_for(c, s);
+  int st = ensure_buf(&w.scores, &w.scores_floats, n_heads * rows, "scratch alloc");
   if (st) return st;
   DecodeGenericArgs g{};
   g.q = dq;
@@ -749,7 +826,7 @@ int run_generic(bnr_ctx *c, const float *dq, const float *dk, const float *dv, l
   g.v_cache = dv;
   g.kv_stride = kv_stride;
   g.out = dout;
-  g.scores = c->scratch;
+  g.scores = w.scores;
   g.n_heads = (int)n_heads;
   g.group = (int)(n_heads / n_kv);
   g.head_dim = (int)head_dim;
@@ -803,7 +880,13 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   DeviceGuard dg(device_id);
   bnr_ctx *c = new bnr_ctx();
   c->device = device_id;
-  c->name = fmt("HIP (%s, %s, device %d)", prop.name, prop.gcnArchName, device_id);
+  // The HIP runtime actually loaded (a process may hold PyTorch's bundled
+  // runtime rather than the system one) goes into the name.
+  int rt = 0, drv = 0;
+  (void)hipRuntimeGetVersion(&rt);
+  (void)hipDriverGetVersion(&drv);
+  c->name = fmt("HIP (%s, %s, device %d; runtime %d, driver %d)", prop.name, prop.gcnArchName,
+                device_id, rt, drv);
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete c;
@@ -822,6 +905,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = std::min(2, std::max(0, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_SPLIT_COST")) c->split_cost = std::max(0, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_ROWS")) c->ref_rows = std::max(0, atoi(v));
+  if (const char *v = std::getenv("BNR_DECODE_REF_WAVES")) c->ref_waves = atoi(v) == 8 ? 8 : 4;
   if (const char *v = std::getenv("BNR_DECODE_PASSES")) c->min_passes = std::min(64, std::max(1, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_RPG")) {
     int r = atoi(v);
@@ -845,12 +929,12 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
       if (m.dev) (void)hipFree(m.dev);
     if (c->d_bytes) (void)hipFree(c->d_bytes);
     if (c->h_stage) (void)hipHostFree(c->h_stage);
-    float *bufs[] = {c->d_cos, c->d_sin, c->ws_o, c->scratch, c->d_q, c->d_k, c->d_out, c->pf_ws};
+    if (c->h_zc) (void)hipHostFree(c->h_zc);
+    float *bufs[] = {c->d_cos, c->d_sin, c->d_q, c->d_out, c->pf_ws};
     for (float *p : bufs)
       if (p) (void)hipFree(p);
-    if (c->ws_ml) (void)hipFree(c->ws_ml);
-    if (c->counters) (void)hipFree(c->counters);
-    if (c->acc) (void)hipFree(c->acc);
+    free_ws(c->hws);
+    free_ws(c->dws);
     if (c->pf_counters) (void)hipFree(c->pf_counters);
     if (c->pf_queue) (void)hipFree(c->pf_queue);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -882,19 +966,17 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
                      fmt("k.len() = %zu", k_len));
   if (q_len + k_len == 0) return set_ok();
   if ((q_len && !q) || (k_len && !k)) return err_backend("rope_embed: NULL slice");
-  // q and k in one pinned copy each way: [q | k], k 16-byte aligned.
+  // q and k rotate in place in the zero-copy staging: [q | k], k 16-byte
+  // aligned.
   const size_t qs = round4(q_len), total = qs + k_len;
-  st = ensure_buf(&c->d_q, &c->d_q_n, total, "staging alloc");
+  st = ensure_zc(c, total);
   if (st) return st;
-  st = ensure_host(c, total);
-  if (st) return st;
-  float *h = c->h_stage;
+  float *h = c->h_zc;
   if (q_len) std::memcpy(h, q, q_len * sizeof(float));
   if (k_len) std::memcpy(h + qs, k, k_len * sizeof(float));
-  HIP_TRY(hipMemcpyAsync(c->d_q, h, total * 4, hipMemcpyHostToDevice, c->stream), "upload q/k");
   RopeAppendArgs a{};
-  a.q = c->d_q;
-  a.k = c->d_q + qs;
+  a.q = c->d_zc;
+  a.k = c->d_zc + qs;
   a.n_tokens = 1;
   a.start_pos = (int)position;
   a.n_heads = (int)n_heads;
@@ -903,8 +985,8 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
   a.cos_tab = c->d_cos;
   a.sin_tab = c->d_sin;
   HIP_TRY(launch_rope_append(a, c->stream), "rope launch");
-  HIP_TRY(hipMemcpyAsync(h, c->d_q, total * 4, hipMemcpyDeviceToHost, c->stream), "download q/k");
-  HIP_TRY(hipStreamSynchronize(c->stream), "rope_embed");
+  st = host_wait(c, "rope_embed");
+  if (st) return st;
   if (q_len) std::memcpy(q, h, q_len * sizeof(float));
   if (k_len) std::memcpy(k, h + qs, k_len * sizeof(float));
   return set_ok();
@@ -973,23 +1055,21 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
   size_t r0 = 0;
   if (c->mirror_mode == BNR_MIRROR_INCREMENTAL && m->synced == cur_pos) r0 = cur_pos;
   if (r0 == cur_pos && cur_pos > 0 && fast_shape(n_heads, n_kv_heads, head_dim)) {
-    // One new row: q and row cur_pos of every kv head go over in one pinned
-    // copy, and the decode kernel appends the row to the mirror itself
-    // (fused append, no rotation).  Device staging: [q | k row | v row | out].
+    // One new row: the decode kernel reads q and row cur_pos of every kv
+    // head from the zero-copy staging, appends the row to the mirror itself
+    // (fused append, no rotation) and writes the output back into the
+    // staging: [q | k row | v row | out].
     const size_t rs = n_kv_heads * head_dim, in_n = q_len + 2 * rs;
-    int st = ensure_buf(&c->d_q, &c->d_q_n, in_n + out_len, "staging alloc");
+    int st = ensure_zc(c, in_n + out_len);
     if (st) return st;
-    st = ensure_host(c, std::max(in_n, out_len));
-    if (st) return st;
-    float *h = c->h_stage, *d = c->d_q;
+    float *h = c->h_zc, *d = c->d_zc;
     std::memcpy(h, q, q_len * sizeof(float));
     for (size_t kh = 0; kh < n_kv_heads; ++kh) {
       const size_t src = kh * head_stride + cur_pos * head_dim;
       std::memcpy(h + q_len + kh * head_dim, k_cache + src, head_dim * sizeof(float));
       std::memcpy(h + q_len + rs + kh * head_dim, v_cache + src, head_dim * sizeof(float));
     }
-    m->synced = 0;  // unknown until the launch and the copies succeed
-    HIP_TRY(hipMemcpyAsync(d, h, in_n * 4, hipMemcpyHostToDevice, c->stream), "upload q/row");
+    m->synced = 0;  // unknown until the launch succeeds
     DecodeArgs a{};
     a.q = d;
     a.k_new = d + q_len;
@@ -1001,9 +1081,9 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     const int p = (int)cur_pos;
     st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), m->rows, c->stream);
     if (st) return st;
-    HIP_TRY(hipMemcpyAsync(h, d + in_n, out_len * 4, hipMemcpyDeviceToHost, c->stream), "download out");
-    HIP_TRY(hipStreamSynchronize(c->stream), "masked_attention");
-    std::memcpy(output, h, out_len * sizeof(float));
+    st = host_wait(c, "masked_attention");
+    if (st) return st;
+    std::memcpy(output, h + in_n, out_len * sizeof(float));
     m->synced = seq_len;
     return set_ok();
   }
@@ -1272,7 +1352,9 @@ extern "C" int bnr_dev_rope_append(bnr_ctx *c, float *q, float *k, const float *
   if (!q || !k || !v || !k_cache || !v_cache) return err_backend("rope_append: NULL pointer");
   std::lock_guard<std::mutex> lk(c->mu);
   DeviceGuard dg(c->device);
-  st = ensure_table(c, start_pos + n_tokens - 1, head_dim, theta);
+  // The table covers every row of the cache, so later calls on it (also
+  // under HIP graph capture) never rebuild it.
+  st = ensure_table(c, std::max(start_pos + n_tokens, cap) - 1, head_dim, theta);
   if (st) return st;
   st = launch_rope_append_dev(c, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
                               k_cache, v_cache, cap, (hipStream_t)stream);
@@ -1308,6 +1390,18 @@ extern "C" int bnr_dev_decode_attention(bnr_ctx *c, const float *q, const float 
   return st ? st : set_ok();
 }
 
+extern "C" int bnr_dev_stream_read(bnr_ctx *c, const void *a, size_t a_bytes, const void *b,
+                                   size_t b_bytes, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if ((a_bytes && !a) || (b_bytes && !b)) return err_backend("stream_read: NULL pointer");
+  if (a_bytes % 16 || b_bytes % 16 || !aligned16(a) || !aligned16(b))
+    return err_shape("16-byte aligned ranges of whole 16-byte words", "an unaligned range");
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_stream_read(a, (long long)a_bytes, b, (long long)b_bytes, (hipStream_t)stream),
+          "stream read launch");
+  return set_ok();
+}
+
 extern "C" int bnr_dev_decode_attention_noalloc(bnr_ctx *c, const float *q, const float *k_cache,
                                                 const float *v_cache, size_t cap, float *out,
                                                 size_t n_heads, size_t n_kv_heads,
@@ -1341,7 +1435,7 @@ extern "C" int bnr_dev_decode_attention_noalloc(bnr_ctx *c, const float *q, cons
   a.positions[0] = (int)cur_pos;
   // Always the reference merge: its state fits the scratch for any context.
   const DecodePlanConfig pc{c->n_cu, c->target_wgs, c->large_wgs, c->force_rpg, c->min_passes,
-                            2,       c->split_cost, c->ref_rows};
+                            2,       c->split_cost, c->ref_rows, c->ref_waves};
   plan_decode(pc, lens, 1, (int)n_kv_heads, a);
   if (a.max_splits > kMaxSplits) return err_backend("decode_attention_noalloc: too many splits");
   a.n_kv = (int)n_kv_heads;
@@ -1364,7 +1458,8 @@ int decode_step_locked(bnr_ctx *c, const float *q, const float *k, const float *
                        float theta, float *k_cache, float *v_cache, size_t cap, float *out,
                        float *q_rot, float *k_rot, hipStream_t s) {
   DeviceGuard dg(c->device);
-  int st = ensure_table(c, position, head_dim, theta);
+  // The table covers every row of the cache (no rebuild on later calls).
+  int st = ensure_table(c, std::max(position + 1, cap) - 1, head_dim, theta);
   if (st) return st;
   const long long kv_stride = (long long)(cap * head_dim);
   const bool al = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
@@ -1389,10 +1484,11 @@ int decode_step_locked(bnr_ctx *c, const float *q, const float *k, const float *
   // Any other shape: rotate copies, append, then the generic kernel.
   const size_t qn = n_heads * head_dim, kn = n_kv_heads * head_dim;
   float *qw = q_rot, *kw = k_rot;
-  st = ensure_buf(&c->d_k, &c->d_k_n, qn + kn, "staging alloc");
+  DecodeWs &w = ws_for(c, s);
+  st = ensure_buf(&w.rot, &w.rot_floats, qn + kn, "staging alloc");
   if (st) return st;
-  if (!qw) qw = c->d_k;
-  if (!kw) kw = c->d_k + qn;
+  if (!qw) qw = w.rot;
+  if (!kw) kw = w.rot + qn;
   HIP_TRY(hipMemcpyAsync(qw, q, qn * 4, hipMemcpyDeviceToDevice, s), "copy q");
   HIP_TRY(hipMemcpyAsync(kw, k, kn * 4, hipMemcpyDeviceToDevice, s), "copy k");
   st = launch_rope_append_dev(c, qw, kw, v, 1, position, n_heads, n_kv_heads, head_dim, k_cache,
@@ -1448,7 +1544,7 @@ extern "C" int bnr_dev_decode_step_batched(bnr_ctx *c, const float *q, const flo
     return err_shape("16-byte aligned device pointers", "an unaligned pointer");
   std::lock_guard<std::mutex> lk(c->mu);
   DeviceGuard dg(c->device);
-  st = ensure_table(c, maxp, head_dim, theta);
+  st = ensure_table(c, std::max<size_t>((size_t)maxp + 1, cap) - 1, head_dim, theta);
   if (st) return st;
   hipStream_t s = (hipStream_t)stream;
   const long long qs = (long long)(n_heads * head_dim), ks = (long long)(n_kv_heads * head_dim);
@@ -1518,13 +1614,26 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
       plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_tiles *= 2);
     pa.n_items = plan.n_items;
     prefill_order(pa);
-    if (plan.split) {
-      st = ensure_buf(&c->pf_ws, &c->pf_ws_floats,
-                      (size_t)n_kv_heads * plan.n_items * group * 66 * 64, "prefill workspace alloc");
+    {
+      // Chunk partials and tickets, sized -- whether this launch splits or
+      // not -- for every split launch on a cache of `cap` rows, so that
+      // later calls on it (also under HIP graph capture) never allocate: at
+      // most T = cap/32 query tiles of at most ceil(T / chunk) chunks each,
+      // and at most kPrefillMaxSplitItems (kv head, item) pairs when the
+      // planner chooses the chunk (a forced chunk size sets its own bound).
+      const long long T = ((long long)cap + 31) / 32;
+      const long long ct = c->pf_chunk_tiles > 0 ? pa.chunk_tiles : kPrefillChunkCandidates[0];
+      long long items = (long long)n_kv_heads * T * ((T + ct - 1) / ct);
+      if (c->pf_chunk_tiles <= 0) items = std::min<long long>(items, kPrefillMaxSplitItems);
+      items = std::max<long long>(items, (long long)n_kv_heads * plan.n_items);
+      st = ensure_buf(&c->pf_ws, &c->pf_ws_floats, (size_t)items * group * 66 * 64,
+                      "prefill workspace alloc");
       if (st) return st;
       st = ensure_zeroed(&c->pf_counters, &c->n_pf_counters,
-                         (size_t)n_kv_heads * pa.n_qtiles * kCounterStride);
+                         (size_t)n_kv_heads * std::max<long long>(T, pa.n_qtiles) * kCounterStride);
       if (st) return st;
+    }
+    if (plan.split) {
       pa.ws = c->pf_ws;
       pa.counters = c->pf_counters;
     }
@@ -1858,17 +1967,18 @@ extern "C" int bnr_rms_norm(bnr_ctx *c, const float *input, size_t in_len, const
   const uint8_t *dw = nullptr;
   st = mirror_bytes(c, weight, w_len * sizeof(float), &dw);
   if (st) return st;
-  st = ensure_buf(&c->d_q, &c->d_q_n, in_len, "staging alloc");
+  // input and output in the zero-copy staging: [input | output]
+  const size_t is = round4(in_len);
+  st = ensure_zc(c, is + in_len);
   if (st) return st;
-  st = ensure_buf(&c->d_out, &c->d_out_n, in_len, "staging alloc");
+  std::memcpy(c->h_zc, input, in_len * sizeof(float));
+  st = run_norm_quant(c, kGluePlain, c->d_zc, nullptr, (const float *)dw, eps, in_len, nullptr,
+                      c->d_zc + is, nullptr, nullptr, nullptr, c->stream);
   if (st) return st;
-  st = put_host(c, c->d_q, {{input, in_len * 4}}, "upload input");
+  st = host_wait(c, "rms_norm");
   if (st) return st;
-  st = run_norm_quant(c, kGluePlain, c->d_q, nullptr, (const float *)dw, eps, in_len, nullptr,
-                      c->d_out, nullptr, nullptr, nullptr, c->stream);
-  if (st) return st;
-  st = get_host(c, output, c->d_out, in_len * 4, "rms_norm");
-  return st ? st : set_ok();
+  std::memcpy(output, c->h_zc + is, in_len * sizeof(float));
+  return set_ok();
 }
 
 extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, const float *up,
@@ -1881,15 +1991,18 @@ extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, cons
   if (!gate || !up || !out) return err_backend("sqrelu_gate: NULL slice");
   std::lock_guard<std::mutex> lk(c->mu);
   DeviceGuard dg(c->device);
-  int st = ensure_buf(&c->d_q, &c->d_q_n, 2 * g_len, "staging alloc");
+  // gate, up and the output in the zero-copy staging: [gate | up | out]
+  const size_t gs = round4(g_len);
+  int st = ensure_zc(c, 3 * gs);
   if (st) return st;
-  st = ensure_buf(&c->d_out, &c->d_out_n, g_len, "staging alloc");
+  float *h = c->h_zc, *d = c->d_zc;
+  std::memcpy(h, gate, g_len * sizeof(float));
+  std::memcpy(h + gs, up, g_len * sizeof(float));
+  HIP_TRY(launch_sqrelu(d, d + gs, d + 2 * gs, (long long)g_len, c->stream), "sqrelu launch");
+  st = host_wait(c, "sqrelu_gate");
   if (st) return st;
-  st = put_host(c, c->d_q, {{gate, g_len * 4}, {up, g_len * 4}}, "upload gate/up");
-  if (st) return st;
-  HIP_TRY(launch_sqrelu(c->d_q, c->d_q + g_len, c->d_out, (long long)g_len, c->stream), "sqrelu launch");
-  st = get_host(c, out, c->d_out, g_len * 4, "sqrelu_gate");
-  return st ? st : set_ok();
+  std::memcpy(out, h + 2 * gs, g_len * sizeof(float));
+  return set_ok();
 }
 
 extern "C" int bnr_dev_rms_norm(bnr_ctx *c, const float *input, const float *weight, float eps,

@@ -271,6 +271,15 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       }
     }
   }
+  // ---- the row groups add through LDS (fast path) ----
+  // Written before the barrier that decides the path (one barrier fewer):
+  // the exact path discards these sums and rewrites s_o after it.
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    st4(&s_o[rg][g][4 * j], olo[g]);
+    st4(&s_o[rg][g][64 + 4 * j], ohi[g]);
+    if (j == 0) s_l[rg][g] = l[g];
+  }
   int over = 0;
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -280,14 +289,6 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   const int gs = a.split_off[b] + s;  // global split index
   float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;
   if (!exact) {
-    // ---- the row groups add through LDS ----
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      st4(&s_o[rg][g][4 * j], olo[g]);
-      st4(&s_o[rg][g][64 + 4 * j], ohi[g]);
-      if (j == 0) s_l[rg][g] = l[g];
-    }
-    __syncthreads();
     for (int e = tid; e < G * D; e += 64 * W) {
       const int g = e / D, dim = e % D;
       float O = s_o[0][g][dim];
@@ -423,6 +424,14 @@ hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s) {
   bool ragged = false;
   for (int b = 0; b < a.batch; ++b)
     ragged |= (a.split_off[b + 1] - a.split_off[b]) != a.max_splits;
+  if (a.ref_waves == 8) {
+    switch (a.group) {
+      case 1: return ragged ? launch_reg_wr<1, 8, true>(a, s) : launch_reg_wr<1, 8, false>(a, s);
+      case 2: return ragged ? launch_reg_wr<2, 8, true>(a, s) : launch_reg_wr<2, 8, false>(a, s);
+      case 4: return ragged ? launch_reg_wr<4, 8, true>(a, s) : launch_reg_wr<4, 8, false>(a, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (a.group) {
     case 1: return ragged ? launch_reg_wr<1, 4, true>(a, s) : launch_reg_wr<1, 4, false>(a, s);
     case 2: return ragged ? launch_reg_wr<2, 4, true>(a, s) : launch_reg_wr<2, 4, false>(a, s);

@@ -75,6 +75,7 @@ struct DecodeArgs {
   // kAccStride floats, zero between launches.
   int merge_ref;
   float *acc;
+  int ref_waves;  // waves per workgroup of the reference-merge kernel: 4 or 8
   int max_splits;                  // largest split count of the launch (grid x)
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
@@ -108,6 +109,8 @@ struct DecodePlanConfig {
   int merge_mode;  // -1: reference merge (default); 0: second kernel; 1: in-kernel ticket; 2: reference merge
   int split_cost;  // planner cost of one split of the in-kernel merges (ns), -1: the mode's default
   int ref_rows;    // reference merge: rows per split (0: planner decides)
+  int ref_waves;   // reference merge, small launches: 4 waves per workgroup if 4, else 8
+                   // (large launches: 4)
 };
 // Split-K plan of one decode launch over sequences of lens[b] rows: fills
 // a.rpg, a.passes, a.rows_per_split, a.batch, a.split_off, a.max_splits and
@@ -126,6 +129,11 @@ struct DecodeGenericArgs {
   float scale;
 };
 hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s);
+
+// Plain streaming read of two device ranges (16-byte multiples), for
+// measurement.
+hipError_t launch_stream_read(const void *a, long long a_bytes, const void *b, long long b_bytes,
+                              hipStream_t s);
 
 // Causal flash prefill (head_dim 128, fp32 MFMA): query i of the n_tokens
 // (position start_pos + i) attends cache rows 0..start_pos+i.

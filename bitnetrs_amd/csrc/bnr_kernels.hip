@@ -646,6 +646,21 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecodeGenericArgs a
   }
 }
 
+// Plain streaming read of two device ranges (the K and V caches of one
+// layer), for measurement: what one launch can read of that many bytes.
+// One 16-byte load per thread over a grid that covers both ranges (the
+// fastest of the shapes measured on MI355X); a workgroup's loads feed a sum
+// that is stored only if it equals an impossible value, so they are kept.
+__global__ __launch_bounds__(512) void stream_read_kernel(const float4 *a, long long na,
+                                                          const float4 *b, long long nb) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i < na) v = a[i];
+  else if (i - na < nb) v = b[i - na];
+  const float sum = (v.x + v.y) + (v.z + v.w);
+  if (sum == -1.2345e-30f && i < na) const_cast<float4 *>(a)[i] = v;
+}
+
 template <int G, bool INLINE, bool RAGGED>
 hipError_t launch_decode_gir(const DecodeArgs &a, hipStream_t s) {
   dim3 grid(a.max_splits, a.n_kv, a.batch), block(256);
@@ -715,6 +730,17 @@ hipError_t launch_decode(const DecodeArgs &a, hipStream_t s) {
     case 8: return launch_decode_g<8>(a, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_stream_read(const void *a, long long a_bytes, const void *b, long long b_bytes,
+                              hipStream_t s) {
+  const long long na = a_bytes / 16, nb = b_bytes / 16;
+  if (na + nb == 0) return hipSuccess;
+  const long long wgs = (na + nb + 511) / 512;
+  if (wgs > 0x7fffffffLL) return hipErrorInvalidValue;
+  stream_read_kernel<<<dim3((unsigned)wgs), dim3(512), 0, s>>>(
+      static_cast<const float4 *>(a), na, static_cast<const float4 *>(b), nb);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s) {

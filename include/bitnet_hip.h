@@ -366,6 +366,14 @@ int bnr_kv_dev_prefill(bnr_ctx *ctx, bnr_kv_cache *cache, size_t layer, float *q
                        const float *v, size_t n_tokens, size_t start_pos, size_t n_heads,
                        float theta, float *out, void *stream);
 
+/* ---- Measurement ---------------------------------------------------------
+ * A plain streaming read of two device ranges (a_bytes at a, b_bytes at b;
+ * 16-byte aligned, multiples of 16), ordered on `stream`: no counterpart in
+ * the reference.  The benchmark times it on the K and V caches a decode step
+ * reads, as the floor a single launch of that many bytes can reach. */
+int bnr_dev_stream_read(bnr_ctx *ctx, const void *a, size_t a_bytes, const void *b,
+                        size_t b_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

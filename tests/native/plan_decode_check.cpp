@@ -2,13 +2,14 @@
 // against libbitnet_hip.so; no GPU is touched.  Prints "ok" or the first
 // violated property.
 //
-// Properties, over 9000 seeded launches (1..64 sequences, 1..8192 rows,
+// Properties, over 9900 seeded launches (1..64 sequences, 1..8192 rows,
 // 1..64 kv heads, the default 256-CU configuration and tuning overrides):
 //  - every plan: 1 <= rpg <= 8, passes >= 1, the split counts are
 //    ceil(len_b / rows_per_split), max_splits is the largest (at most
 //    kMaxSplits);
-//  - reference merge (the default): rows_per_split fits its passes
-//    (16*rpg*(passes-1) < rows <= 16*rpg*passes), rpg <= 6 (<= 4 for large
+//  - reference merge (the default): rows_per_split fits its passes of
+//    4*waves*rpg rows (8 waves and rpg <= 3 for small launches, or 4 waves
+//    and rpg <= 6 when configured; 4 waves and rpg <= 4 for large
 //    launches), at least 16 rows; the launch fits its target (one workgroup
 //    per CU, eight for large launches) whenever one split per (sequence,
 //    kv head) does, and no smaller split size would fit it;
@@ -66,9 +67,13 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
   if (c.merge_mode < 0 || c.merge_mode == 2) {
     if (!a.merge_ref || !a.merge_inline) return fail("reference merge chosen", L0, batch, n_kv);
     if (rows < 16) return fail("at least 16 rows", L0, batch, n_kv);
-    if (!(16 * a.rpg * (a.passes - 1) < rows && rows <= 16 * a.rpg * a.passes))
+    const int waves = large || c.ref_waves == 4 ? 4 : 8;
+    const int nrg = 4 * waves;  // row groups of a workgroup
+    if (a.ref_waves != waves) return fail("reference waves", L0, batch, n_kv);
+    if (!(nrg * a.rpg * (a.passes - 1) < rows && rows <= nrg * a.rpg * a.passes))
       return fail("rows fit the passes", L0, batch, n_kv);
-    if (c.force_rpg == 0 && a.rpg > (large ? 4 : 6)) return fail("reference rpg bound", L0, batch, n_kv);
+    if (c.force_rpg == 0 && a.rpg > (large ? 4 : waves == 8 ? 3 : 6))
+      return fail("reference rpg bound", L0, batch, n_kv);
     if (c.ref_rows > 0) return 0;
     const long long target = large ? 8LL * c.target_wgs : c.target_wgs;
     const bool feasible = (long long)batch * n_kv <= target;
@@ -83,8 +88,8 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
       const int r0 = smallest;
       const int rpg = a.rpg;
       // the plan is the smallest fitting size rounded up to whole passes
-      const int passes = (r0 + 16 * rpg - 1) / (16 * rpg);
-      if (rows != 16 * rpg * passes && rows != r0)
+      const int passes = (r0 + nrg * rpg - 1) / (nrg * rpg);
+      if (rows != nrg * rpg * passes && rows != r0)
         return fail("reference split is not the smallest fitting one", L0, batch, n_kv);
     }
     return 0;
@@ -101,7 +106,8 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
     if (feasible && wgs > c.target_wgs) return fail("small launch over target", L0, batch, n_kv);
     if (feasible) {
       long long best = -1;
-      for (int p = c.min_passes; p <= (max_len + 15) / 16 && p <= 4096; ++p)
+      const int p_max = (max_len + 15) / 16 > c.min_passes ? (max_len + 15) / 16 : c.min_passes;
+      for (int p = c.min_passes; p <= p_max && p <= 4096; ++p)
         for (int r = 1; r <= 8; ++r) {
           if (!a.merge_inline && (r & (r - 1))) continue;
           const int R = 16 * r * p;
@@ -123,12 +129,12 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
 }
 
 int main() {
-  const DecodePlanConfig def{256, 256, 1024, 0, 1, -1, -1, 0};
-  const DecodePlanConfig ticket{256, 256, 1024, 0, 1, 1, -1, 0};
+  const DecodePlanConfig def{256, 256, 1024, 0, 1, -1, -1, 0, 8};
+  const DecodePlanConfig ticket{256, 256, 1024, 0, 1, 1, -1, 0, 8};
   // The 2B shape, one sequence: the plans of both merges.
   struct Want { int L, rpg, passes, rows; };
-  const Want want_ref[] = {{512, 1, 1, 16},   {2048, 3, 1, 48},  {4096, 6, 1, 96},
-                           {8192, 6, 2, 192}, {32768, 6, 7, 672}};
+  const Want want_ref[] = {{512, 1, 1, 32},   {2048, 2, 1, 64},  {4096, 3, 1, 96},
+                           {8192, 3, 2, 192}, {32768, 3, 7, 672}};
   for (const Want &w : want_ref) {
     DecodeArgs a{};
     plan_decode(def, &w.L, 1, 5, a);
@@ -152,15 +158,16 @@ int main() {
   }
   std::mt19937 rng(0xB17E);
   const DecodePlanConfig cfgs[] = {def,
-                                   {256, 128, 1024, 0, 1, -1, -1, 0},   // a smaller target
-                                   {256, 256, 1024, 3, 1, -1, -1, 0},   // forced rpg
-                                   {256, 256, 1024, 0, 1, -1, -1, 200}, // forced split size
-                                   {128, 128, 512, 0, 1, -1, -1, 0},    // a smaller device
+                                   {256, 128, 1024, 0, 1, -1, -1, 0, 4},   // a smaller target
+                                   {256, 256, 1024, 3, 1, -1, -1, 0, 4},   // forced rpg
+                                   {256, 256, 1024, 0, 1, -1, -1, 200, 4}, // forced split size
+                                   {128, 128, 512, 0, 1, -1, -1, 0, 4},    // a smaller device
+                                   {256, 256, 1024, 0, 1, -1, -1, 0, 4},   // four waves
                                    ticket,
-                                   {256, 256, 1024, 0, 2, 1, -1, 0},    // ticket, at least two passes
-                                   {256, 128, 1024, 0, 1, 1, -1, 0},    // ticket, a smaller target
-                                   {256, 256, 1024, 0, 1, 0, -1, 0},    // forced two-launch merge
-                                   {256, 256, 1024, 6, 1, 1, -1, 0}};   // ticket, forced rpg
+                                   {256, 256, 1024, 0, 2, 1, -1, 0, 4},    // ticket, at least two passes
+                                   {256, 128, 1024, 0, 1, 1, -1, 0, 4},    // ticket, a smaller target
+                                   {256, 256, 1024, 0, 1, 0, -1, 0, 4},    // forced two-launch merge
+                                   {256, 256, 1024, 6, 1, 1, -1, 0, 4}};  // ticket, forced rpg
   int n = 0;
   for (const DecodePlanConfig &c : cfgs) {
     for (int t = 0; t < 900; ++t) {

@@ -2,10 +2,10 @@
 splits weigh their rows against the score of the newest row and add their
 sums with device-scope atomics.  Covers the plain case over the planner's
 range, consecutive launches on one context (the accumulators must come back
-to zero), and the exact path: splits whose scores run more than 2^64 above
-the reference keep their own maximum and are folded in by the merging
-workgroup.  Planted rows make single splits, several splits, the newest
-row's own split and every split take it.
+to zero), both workgroup shapes (8 and 4 waves), and the exact path: splits
+whose scores run more than 2^64 above the reference keep their own maximum
+and are folded in by the merging workgroup.  Planted rows make single
+splits, several splits, the newest row's own split and every split take it.
 References: the oracle's rope_embed -> store_kv -> masked_attention
 (bitnet-cpu/src/rope.rs:414-430, bitnet-model/src/lib.rs:184-236,
 bitnet-cpu/src/attention.rs:97-209)."""
@@ -39,11 +39,14 @@ def host(t):
     return t.cpu().numpy()
 
 
-@pytest.fixture
-def ref_backend(monkeypatch):
+@pytest.fixture(params=[8, 4], ids=["8waves", "4waves"])
+def ref_backend(monkeypatch, request):
+    # Small launches run 8-wave workgroups by default; the 4-wave kernel (the
+    # large launches' one) is forced on the same cases.
     import bitnetrs_amd
 
     monkeypatch.setenv("BNR_DECODE_MERGE", "2")
+    monkeypatch.setenv("BNR_DECODE_REF_WAVES", str(request.param))
     be = bitnetrs_amd.HipBackend(0)
     yield be
     be.close()
