@@ -602,11 +602,12 @@ int ensure_table(bnr_ctx *c, size_t position, size_t head_dim, float theta) {
                       std::fabs(c->tab_theta - theta) > 1e-3f || position >= c->tab_len;
   if (!reinit) return BNR_OK;
   size_t len = std::max<size_t>(position + 1, 4096);
-  // A position past the end of a table of the same head_dim and theta grows
-  // it geometrically.  Entries depend on (position, i) only, so every value
-  // is the one the reference's max(position + 1, 4096) table holds; only the
-  // rebuild on every call past the end is saved.
-  if (c->tab_valid && c->tab_head_dim == head_dim && std::fabs(c->tab_theta - theta) <= 1e-3f)
+  // A position past the end of a table of the same head_dim and exactly the
+  // same theta grows it geometrically.  Entries depend on (position, i,
+  // theta) only, so every value is the one the reference's max(position + 1,
+  // 4096) table holds; only the rebuild on every call past the end is saved.
+  // Any other theta rebuilds at max(position + 1, 4096), as the reference.
+  if (c->tab_valid && c->tab_head_dim == head_dim && c->tab_theta == theta)
     len = std::max(len, 2 * c->tab_len);
   return build_table(c, len, head_dim, theta);
 }
@@ -1159,7 +1160,7 @@ extern "C" int bnr_mirror_invalidate(bnr_ctx *c) {
 // ---------------------------------------------------------------------------
 namespace {
 
-// Checks of gemv::ternary_gemv_quantised (bitnet-cpu/src/gemv.rs:384-420),
+// Checks of gemv::ternary_gemv_quantised (bitnet-cpu/src/gemv.rs:260-295),
 // in its order, for the lengths that are given (SIZE_MAX: not checked).
 int check_gemv(size_t weight_len, float weight_scale, size_t act_len, float act_absmax,
                size_t out_len, size_t out_features, size_t in_features) {
@@ -1194,7 +1195,7 @@ int run_gemv(const uint8_t *w, float weight_scale, const int8_t *act, float act_
   a.packed_cols = (long long)((in_features + 3) / 4);
   a.out_features = (int)out_features;
   a.in_features = (int)in_features;
-  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), f32, left to right
+  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:297), f32, left to right
   volatile float ws_as = weight_scale * act_absmax;
   a.scale = ws_as / 127.0f;
   const bool vec = a.packed_cols % 16 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)act % 16) == 0;

@@ -4,7 +4,7 @@
 // stored 2 bits per weight (row-aligned, ceil(K/4) bytes per row; code
 // 0b00 -> +1, 0b01 -> 0, 0b10 -> -1, 0b11 -> 0, weight 4b+p at bits 2p of
 // byte b) and a[] int8.  The integer sum is exact, so the result is
-// bit-identical to the reference's (bitnet-cpu/src/gemv.rs:368-430).
+// bit-identical to the reference's (bitnet-cpu/src/gemv.rs:251-310).
 //
 // Memory-bound: each packed weight byte is read once.  A workgroup owns 16
 // rows, 16 lanes per row; a lane takes the row's 16-byte pieces j, j+16, ...
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
     }
   }
   if (a.act_absmax_dev) {
-    // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), f32, left to right
+    // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:297), f32, left to right
     const float t = ws * *a.act_absmax_dev;
     scale = t / 127.0f;
   }
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
     }
   }
   acc = row_sum16_i(acc);
-  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:423), act_scale = scale * 127
+  // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:297), act_scale = scale * 127
   const float t = ws * (scale * 127.0f);
   const float cs = t / 127.0f;
   if (j == 0 && row < m) out[row] = (float)acc * cs;

@@ -102,13 +102,13 @@ int bnr_mirror_invalidate(bnr_ctx *ctx);
 
 /* Backend::ternary_gemv_preq (bitnet-core/src/backend/mod.rs:445-468), as
  * CpuBackend implements it (bitnet-cpu/src/lib.rs:519-538 ->
- * gemv::ternary_gemv_quantised, bitnet-cpu/src/gemv.rs:368-430):
+ * gemv::ternary_gemv_quantised, bitnet-cpu/src/gemv.rs:251-310):
  *   output[i] = (float)(sum_j W[i][j] * activation_q[j])
  *               * (weight_scale * act_absmax / 127)
  * with W packed 2 bits per weight, row-aligned (ceil(in_features/4) bytes
  * per row; 0b00 -> +1, 0b01 -> 0, 0b10 -> -1, 0b11 -> 0).  The integer sum
  * is exact, so outputs are bit-identical to the reference's.  Validation
- * order and messages follow gemv.rs:384-420 (InvalidShape for lengths,
+ * order and messages follow gemv.rs:260-295 (InvalidShape for lengths,
  * QuantizationError for scales).  The weight matrix is mirrored in HBM on
  * first use, keyed by (weight_packed, weight_len) and a 64-byte sample of
  * its contents: model weights are immutable once loaded.  After rewriting a

@@ -331,7 +331,7 @@ def dot_packed_ternary_i8(packed: np.ndarray, act: np.ndarray, n: int) -> int:
 def ternary_gemv_preq(weight_packed, weight_scale, activation_q, act_absmax, output,
                       out_features, in_features) -> None:
     """CpuBackend::ternary_gemv_preq (bitnet-cpu/src/lib.rs:519-538 ->
-    gemv::ternary_gemv_quantised, gemv.rs:368-430)."""
+    gemv::ternary_gemv_quantised, gemv.rs:251-310)."""
     w = np.ascontiguousarray(weight_packed, np.uint8).reshape(-1)
     a = np.ascontiguousarray(activation_q, np.int8).reshape(-1)
     _check(lib().bnro_ternary_gemv_preq(_bytes_ptr(w, np.uint8), w.size, weight_scale,

@@ -679,7 +679,7 @@ int32_t bnro_dot_packed_ternary_i8(const uint8_t *packed, const int8_t *act, siz
   return total;
 }
 
-/* gemv.rs:368-430 (validation order and messages as there). */
+/* gemv.rs:251-310 (validation order and messages as there). */
 int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, float weight_scale,
                            const int8_t *activation_q, size_t act_len, float act_absmax,
                            float *output, size_t out_len, size_t out_features,

@@ -117,7 +117,7 @@ int bnro_pack_ternary(const int8_t *w, size_t n, uint8_t *out);
  * DECODE_LUT 390-404 with code 0b11 -> 0, dot_ternary_i8_avx2 118-171):
  * exact i32 sum of decoded weight x activation over n elements. */
 int32_t bnro_dot_packed_ternary_i8(const uint8_t *packed, const int8_t *act, size_t n);
-/* gemv::ternary_gemv_quantised  bitnet-cpu/src/gemv.rs:368-430, which is
+/* gemv::ternary_gemv_quantised  bitnet-cpu/src/gemv.rs:251-310, which is
  * CpuBackend::ternary_gemv_preq (bitnet-cpu/src/lib.rs:519-538):
  * out[i] = (float)dot(W[i], act) * (weight_scale * act_absmax / 127). */
 int bnro_ternary_gemv_preq(const uint8_t *weight_packed, size_t weight_len, float weight_scale,

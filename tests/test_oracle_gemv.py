@@ -1,7 +1,7 @@
 """Pins of the oracle's W2A8 ternary GEMV (oracle/bnr_oracle.c,
 bnro_ternary_gemv_preq / bnro_dot_packed_ternary_i8 / bnro_pack_ternary).
 
-Closed forms are the reference's own tests (bitnet-cpu/src/gemv.rs:420-728,
+Closed forms are the reference's own tests (bitnet-cpu/src/gemv.rs:318-728,
 restated for the pre-quantised entry point with act_absmax = 127 so that the
 combined scale equals weight_scale); brute force is an independent numpy
 computation from the unpacked int8 matrix.  Integer accumulation is exact, so
@@ -120,7 +120,7 @@ def test_gemv_errors_match_reference():
         oracle.ternary_gemv_preq(p, 1.0, x, float("nan"), out, 2, 3)
     with pytest.raises(oracle.QuantizationError, match="act_scale must be finite > 0, got inf"):
         oracle.ternary_gemv_preq(p, 1.0, x, float("inf"), out, 2, 3)
-    # shape errors come before scale errors (gemv.rs:384-420)
+    # shape errors come before scale errors (gemv.rs:260-295)
     with pytest.raises(oracle.InvalidShape):
         oracle.ternary_gemv_preq(p, 0.0, np.zeros(4, np.int8), 1.0, out, 2, 3)
 
