@@ -158,6 +158,11 @@ struct DeviceGuard {
 
 constexpr size_t kMaxMirrors = 256;
 
+// Tiled prefill launches: planned key chunks on a grid of items, the same
+// items from a queue of resident workgroups, stream-K runs, or (auto, the
+// default) stream-K or the grid by shape.
+constexpr int kPrefillGrid = 0, kPrefillQueue = 1, kPrefillStreamK = 2, kPrefillAuto = 3;
+
 // Merge state of split-K decode launches: split partials (exact path),
 // tickets and reference-merge accumulators.  Kernels leave tickets and
 // accumulators at zero after every launch; launches that share a workspace
@@ -235,7 +240,8 @@ struct bnr_ctx {
   // prefill planner
   int n_cu = 256;
   int pf_chunk_tiles = -1;  // -1: planner decides; else key tiles per chunk
-  int pf_persistent = 0;    // 1: resident workgroups take prefill items from a queue
+  int pf_mode = kPrefillAuto;  // tiled prefill launch: kPrefillAuto / Grid / Queue / StreamK
+  int pf_sk_wgs = 0;              // stream-K workgroups (0: every resident slot)
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
 
@@ -914,7 +920,13 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   }
   if (const char *v = std::getenv("BNR_PREFILL_CHUNK_TILES"))
     c->pf_chunk_tiles = std::min(std::max(atoi(v), 1), kPrefillNoSplit);
-  if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT")) c->pf_persistent = atoi(v) > 0;
+  if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT"))
+    if (atoi(v) > 0) c->pf_mode = kPrefillQueue;
+  if (const char *v = std::getenv("BNR_PREFILL_SK_WGS")) c->pf_sk_wgs = std::max(atoi(v), 0);
+  if (const char *v = std::getenv("BNR_PREFILL_MODE")) {
+    const int m = atoi(v);
+    if (m >= kPrefillGrid && m <= kPrefillAuto) c->pf_mode = m;
+  }
   *out = c;
   return set_ok();
 }
@@ -1607,26 +1619,41 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
     pa.n_kv = (int)n_kv_heads;
     pa.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
     pa.n_qtiles = (int)((n_tokens + 31) / 32);
-    pa.chunk_tiles = c->pf_chunk_tiles > 0
-                         ? c->pf_chunk_tiles
-                         : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads);
+    const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
+    // Stream-K where every query tile has about as many keys as the next
+    // (a cached prefix at least as long as the new tokens: 512 queries after
+    // 1536 cached rows 98 vs 100 us, 1024 after 3000 303 vs 312 us on
+    // MI355X); planned key chunks otherwise (N = 1024 from an empty cache:
+    // 73 vs 85 us, N = 4096: 676 vs 710 us).
+    const bool streamk = c->pf_chunk_tiles <= 0 &&
+                         (c->pf_mode == kPrefillStreamK ||
+                          (c->pf_mode == kPrefillAuto && start_pos >= n_tokens));
+    if (!streamk) {
+      pa.chunk_tiles = c->pf_chunk_tiles > 0
+                           ? c->pf_chunk_tiles
+                           : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads);
+    } else {
+      pa.chunk_tiles = kPrefillNoSplit;
+    }
     PrefillPlan plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_tiles);
     while (plan.n_items > 65535)  // grid y limit
       plan = prefill_plan((int)n_tokens, (int)start_pos, pa.chunk_tiles *= 2);
     pa.n_items = plan.n_items;
     prefill_order(pa);
     {
-      // Chunk partials and tickets, sized -- whether this launch splits or
-      // not -- for every split launch on a cache of `cap` rows, so that
-      // later calls on it (also under HIP graph capture) never allocate: at
-      // most T = cap/32 query tiles of at most ceil(T / chunk) chunks each,
-      // and at most kPrefillMaxSplitItems (kv head, item) pairs when the
-      // planner chooses the chunk (a forced chunk size sets its own bound).
+      // Partial states and tickets, sized -- whatever this launch needs --
+      // for every launch on a cache of `cap` rows, so that later calls on it
+      // (also under HIP graph capture) never allocate: stream-K launches keep
+      // two states per resident workgroup; chunked launches at most T =
+      // cap/32 query tiles of at most ceil(T / chunk) chunks each, and at
+      // most kPrefillMaxSplitItems (kv head, item) pairs when the planner
+      // chooses the chunk (a forced chunk size sets its own bound).
       const long long T = ((long long)cap + 31) / 32;
       const long long ct = c->pf_chunk_tiles > 0 ? pa.chunk_tiles : kPrefillChunkCandidates[0];
       long long items = (long long)n_kv_heads * T * ((T + ct - 1) / ct);
       if (c->pf_chunk_tiles <= 0) items = std::min<long long>(items, kPrefillMaxSplitItems);
       items = std::max<long long>(items, (long long)n_kv_heads * plan.n_items);
+      items = std::max<long long>(items, 2LL * c->n_cu * per_cu);
       st = ensure_buf(&c->pf_ws, &c->pf_ws_floats, (size_t)items * group * 66 * 64,
                       "prefill workspace alloc");
       if (st) return st;
@@ -1634,16 +1661,26 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
                          (size_t)n_kv_heads * std::max<long long>(T, pa.n_qtiles) * kCounterStride);
       if (st) return st;
     }
+    if (streamk) {
+      // Equal runs of tile products over the resident workgroups.
+      prefill_streamk_units(pa);
+      pa.ws = c->pf_ws;
+      pa.counters = c->pf_counters;
+      const long long slots = c->pf_sk_wgs > 0 ? std::min(c->pf_sk_wgs, c->n_cu * per_cu)
+                                                : (long long)c->n_cu * per_cu;
+      const int wgs = (int)std::min<long long>(pa.sk_units, slots);
+      HIP_TRY(launch_prefill_streamk(pa, group, wgs, s), "prefill launch");
+      return set_ok();
+    }
     if (plan.split) {
       pa.ws = c->pf_ws;
       pa.counters = c->pf_counters;
     }
     int pwgs = 0;
-    if (c->pf_persistent > 0) {
+    if (c->pf_mode == kPrefillQueue) {
       st = ensure_zeroed(&c->pf_queue, &c->n_pf_queue, 2 * kCounterStride);
       if (st) return st;
       pa.queue = c->pf_queue;
-      const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
       pwgs = (int)std::min<long long>((long long)n_kv_heads * plan.n_items, (long long)c->n_cu * per_cu);
     }
     HIP_TRY(launch_prefill(pa, group, pwgs, s), "prefill launch");

@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <cmath>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -160,6 +162,11 @@ struct PrefillArgs {
   // of one tile consecutive.
   int lpt, n_full;
   int part_off[64];
+  // Stream-K launch (sk_units > 0): units = (kv head, query tile, key tile)
+  // tile products in that order, sk_per_head of them per kv head; the
+  // launch's workgroups take equal runs of them.  ws then holds two partial
+  // states per workgroup: [2 * workgroups][G][66][64].
+  long long sk_units, sk_per_head;
 };
 constexpr int kMaxLptChunk = 64;
 constexpr int kPrefillNoSplit = 1 << 20;  // chunk_tiles of an unsplit launch
@@ -266,7 +273,50 @@ PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_tiles);
 // a.n_qtiles and a.chunk_tiles.
 void prefill_order(PrefillArgs &a);
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.
+// Stream-K runs: workgroup w of P takes units [sk_u0(w), sk_u0(w + 1)), a
+// sequence of segments (the key tiles of one query tile within the run).
+struct SkSeg {
+  int h, qt, kt0, kt1, nk;  // key tiles kt0 .. kt1-1 of query tile qt (nk tiles) of kv head h
+  long long qstart;         // unit of the query tile's key tile 0
+};
+
+__host__ __device__ inline long long sk_off(long long qt, int A) {
+  return A * qt + qt * (qt - 1) / 2;  // units of query tiles 0 .. qt-1 of a head
+}
+__host__ __device__ inline long long sk_u0(int w, long long U, int P) {
+  return (long long)w * U / P;
+}
+__host__ __device__ inline int sk_wg_of(long long u, long long U, int P) {
+  return (int)(((u + 1) * P - 1) / U);  // the run holding unit u
+}
+
+// The segment starting at unit u of a run ending at uend.
+__host__ __device__ inline SkSeg sk_seg(const PrefillArgs &a, long long u, long long uend) {
+  const int nqt = a.n_qtiles, A = (a.start_pos + 31) / 32 + 1;
+  const int nt_last = (a.start_pos + a.n_tokens - 1) / 32 + 1;
+  SkSeg sg;
+  sg.h = (int)(u / a.sk_per_head);
+  const long long off = u - (long long)sg.h * a.sk_per_head;
+  // largest qt with sk_off(qt) <= off: the quadratic's root, then exact fix-ups
+  const double b = 2.0 * A - 1.0;
+  int qt = (int)((sqrt(b * b + 8.0 * (double)off) - b) * 0.5);
+  qt = qt < 0 ? 0 : (qt > nqt - 1 ? nqt - 1 : qt);
+  while (qt + 1 < nqt && sk_off(qt + 1, A) <= off) ++qt;
+  while (qt > 0 && sk_off(qt, A) > off) --qt;
+  sg.qt = qt;
+  sg.nk = qt + 1 < nqt ? A + qt : nt_last;
+  sg.kt0 = (int)(off - sk_off(qt, A));
+  sg.kt1 = (int)(sg.kt0 + (uend - u) < sg.nk ? sg.kt0 + (uend - u) : sg.nk);
+  sg.qstart = u - sg.kt0;
+  return sg;
+}
+
 hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, hipStream_t s);
+// Stream-K prefill over `wgs` workgroups (a.sk_units, a.sk_per_head set by
+// prefill_streamk_units).
+hipError_t launch_prefill_streamk(const PrefillArgs &a, int group, int wgs, hipStream_t s);
+// Units of a stream-K launch: sets a.sk_per_head and a.sk_units.
+void prefill_streamk_units(PrefillArgs &a);
 bool prefill_supported(int group);
 
 // W2A8 ternary GEMV: out[i] = (float)dot(W[i], act) * scale, W packed 2 bits

@@ -391,9 +391,211 @@ void prefill_persistent_kernel(PrefillArgs a) {
     }
   }
 }
+// ---------------------------------------------------------------------------
+// Stream-K prefill.  A launch's work is U = n_kv * T units, one unit being a
+// (kv head, query tile, key tile) tile product, T the key tiles of all query
+// tiles of a head.  Units are ordered (kv head, query tile, key tile) and
+// workgroup w of P takes units [w*U/P, (w+1)*U/P): the same number of tile
+// products (+-1) for every workgroup, so the resident workgroups of a
+// launch finish together, with no tail of short items.  A workgroup's run
+// is a sequence of segments: the key tiles of one query tile that fall in
+// the run.  A segment holding a whole query tile writes its output; the
+// others store their partial state -- slot 2w for the run's first segment,
+// 2w+1 for its last -- and take the query tile's ticket, and the last of
+// its parts (workgroups wf..wl, one segment each) merges the others.  As in
+// the persistent kernel, the next segment's first K/V tile and Q fragment
+// are loaded during the current segment's last tile.
+//
+// Workgroup index -> run: runs go to the XCDs in blocks (XCD x, which gets
+// workgroups x, x+8, ..., runs the x-th eighth of the units), so that one
+// XCD's L2 sees the K/V tiles of few kv heads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ PfItem sk_item(const SkSeg &sg) {
+  PfItem it{};
+  it.h = sg.h;
+  it.qt = sg.qt;
+  it.q0 = 32 * sg.qt;
+  it.kt0 = sg.kt0;
+  it.nkt = sg.kt1;
+  return it;
+}
+
+// Output of a whole query tile (normalised O^T, lane layout of pf_finish).
+template <int G>
+__device__ __forceinline__ void sk_store_out(const PrefillArgs &a, int h, int qt,
+                                             const floatx16 (&O)[4], float l) {
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int q0 = 32 * qt;
+  const float inv = 1.0f / (l + __shfl_xor(l, 32));
+  if (q0 + col < a.n_tokens) {
+    float *op = a.out + ((long long)(q0 + col) * a.n_heads + h * G + g) * kHeadDim + 16 * hl;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      st4(op + 32 * (r >> 2) + 4 * (r & 3),
+          make_float4(O[0][r] * inv, O[1][r] * inv, O[2][r] * inv, O[3][r] * inv));
+  }
+}
+
+// Partial state of a split query tile in slot `slot`: 16 float4 of O per
+// lane (register r of the four dim blocks), then (m, l); lane-contiguous.
+// Plain stores: the merge runs in the next kernel.
+__device__ __forceinline__ float *sk_slot(const PrefillArgs &a, int slot, int G, int g) {
+  return a.ws + ((long long)slot * G + g) * 66 * 64;
+}
+
+// End of a segment: a whole query tile writes its output; a part of a split
+// one stores its partial state for prefill_sk_merge_kernel.
+template <int G>
+__device__ __forceinline__ void sk_finish(const PrefillArgs &a, const SkSeg &sg, int w,
+                                          const floatx16 (&O)[4], float m, float l) {
+  if (sg.kt0 == 0 && sg.kt1 == sg.nk) {
+    sk_store_out<G>(a, sg.h, sg.qt, O, l);
+    return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int slot = 2 * w + (sk_u0(w, a.sk_units, gridDim.x) >= sg.qstart ? 0 : 1);
+  float *p = sk_slot(a, slot, G, g);
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    st4(p + (r * 64 + lane) * 4, make_float4(O[0][r], O[1][r], O[2][r], O[3][r]));
+  *reinterpret_cast<float2 *>(p + 64 * 64 + lane * 2) = make_float2(m, l);
+}
+
+// Merge of the split query tiles of a stream-K launch (P = its workgroup
+// count): workgroup (qt, h), wave g merges the parts wf..wl of query tile qt
+// of kv head h, head g, in run order, and writes the output.  Query tiles
+// that one run held whole were written by it; their workgroups exit.
+template <int G>
+__global__ __launch_bounds__(64 * G) void prefill_sk_merge_kernel(PrefillArgs a, int P) {
+  const int qt = blockIdx.x, h = blockIdx.y;
+  const int nqt = a.n_qtiles, A = (a.start_pos + 31) / 32 + 1;
+  const int nt_last = (a.start_pos + a.n_tokens - 1) / 32 + 1;
+  const int nk = qt + 1 < nqt ? A + qt : nt_last;
+  const long long U = a.sk_units;
+  const long long qs = (long long)h * a.sk_per_head + sk_off(qt, A);
+  const int wf = sk_wg_of(qs, U, P), wl = sk_wg_of(qs + nk - 1, U, P);
+  if (wf == wl) return;
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  floatx16 O[4];
+  float m = -1e30f, l = 0.f;
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+  for (int w = wf; w <= wl; ++w) {
+    const int slot = 2 * w + (sk_u0(w, U, P) >= qs ? 0 : 1);
+    const float *p = sk_slot(a, slot, G, g);
+    float4 ov[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ov[r] = ld4(p + (r * 64 + lane) * 4);
+    const float2 ml = *reinterpret_cast<const float2 *>(p + 64 * 64 + lane * 2);
+    const float mn = fmaxf(m, ml.x);
+    const float sa = fast_exp2(m - mn), sb = fast_exp2(ml.x - mn);
+    l = l * sa + ml.y * sb;
+    m = mn;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      O[0][r] = O[0][r] * sa + ov[r].x * sb;
+      O[1][r] = O[1][r] * sa + ov[r].y * sb;
+      O[2][r] = O[2][r] * sa + ov[r].z * sb;
+      O[3][r] = O[3][r] * sa + ov[r].w * sb;
+    }
+  }
+  sk_store_out<G>(a, h, qt, O, l);
+}
+
+template <int G>
+__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_streamk_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) float sK0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sK1[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV1[kPrefillTile];
+  const int P = gridDim.x, b = blockIdx.x;
+  const int w = P % 8 == 0 ? (b % 8) * (P / 8) + b / 8 : b;  // XCD b % 8 runs the (b % 8)-th eighth
+  const long long U = a.sk_units, u_end = sk_u0(w + 1, U, P);
+  long long u = sk_u0(w, U, P);  // first unit of the current segment
+  if (u >= u_end) return;
+  SkSeg sg = sk_seg(a, u, u_end);
+  pf_copy_tile<G>(a, sg.h, sg.kt0, sK0, sV0);
+  float qf[64];
+  pf_load_q<G>(a, sk_item(sg), qf);
+  pf_scale_q(qf, a.scale_log2);
+  wait_vmem();
+  __syncthreads();
+  floatx16 O[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+  float m = -1e30f, l = 0.f;
+  int kt = sg.kt0;
+  // One tile of the current segment on (dk, dv); the next tile, or the next
+  // segment's first, is copied into (nk, nv).  False once the run is done.
+  auto step = [&](const float *dk, const float *dv, float *nk, float *nv) -> bool {
+    const bool lastt = kt + 1 == sg.kt1;
+    const long long un = u + (sg.kt1 - sg.kt0);  // first unit of the next segment
+    const bool more = lastt && un < u_end;
+    const SkSeg ns = more ? sk_seg(a, un, u_end) : sg;
+    if (!lastt) pf_copy_tile<G>(a, sg.h, kt + 1, nk, nv);
+    else if (more) pf_copy_tile<G>(a, ns.h, ns.kt0, nk, nv);
+    const floatx16 S = pf_tile_s(dk, qf);
+    pf_tile_pv(a, sk_item(sg), kt, S, dv, O, m, l);
+    if (more) pf_load_q<G>(a, sk_item(ns), qf);  // qf is no longer read by this segment
+    if (lastt) sk_finish<G>(a, sg, w, O, m, l);
+    wait_vmem();  // this wave's copies (next tile, next Q) have landed
+    __syncthreads();
+    if (!lastt) {
+      ++kt;
+      return true;
+    }
+    if (!more) return false;
+    sg = ns;
+    u = un;
+    kt = sg.kt0;
+    pf_scale_q(qf, a.scale_log2);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) O[db] = floatx16{};
+    m = -1e30f;
+    l = 0.f;
+    return true;
+  };
+  for (;;) {
+    if (!step(sK0, sV0, sK1, sV1)) break;
+    if (!step(sK1, sV1, sK0, sV0)) break;
+  }
+}
 #pragma clang diagnostic pop
 
 }  // namespace
+
+void prefill_streamk_units(PrefillArgs &a) {
+  const long long nqt = a.n_qtiles, A = (a.start_pos + 31) / 32 + 1;
+  const long long nt_last = (a.start_pos + a.n_tokens - 1) / 32 + 1;
+  a.sk_per_head = A * (nqt - 1) + (nqt - 1) * (nqt - 2) / 2 + nt_last;
+  a.sk_units = a.sk_per_head * a.n_kv;
+}
+
+hipError_t launch_prefill_streamk(const PrefillArgs &a, int group, int wgs, hipStream_t s) {
+  if (a.n_tokens <= 0) return hipSuccess;
+  if (wgs <= 0 || a.sk_units < wgs || !a.ws) return hipErrorInvalidValue;
+  const dim3 grid(wgs), mgrid(a.n_qtiles, a.n_kv);
+  switch (group) {
+    case 2:
+      prefill_streamk_kernel<2><<<grid, dim3(128), 0, s>>>(a);
+      prefill_sk_merge_kernel<2><<<mgrid, dim3(128), 0, s>>>(a, wgs);
+      break;
+    case 4:
+      prefill_streamk_kernel<4><<<grid, dim3(256), 0, s>>>(a);
+      prefill_sk_merge_kernel<4><<<mgrid, dim3(256), 0, s>>>(a, wgs);
+      break;
+    case 8:
+      prefill_streamk_kernel<8><<<grid, dim3(512), 0, s>>>(a);
+      prefill_sk_merge_kernel<8><<<mgrid, dim3(512), 0, s>>>(a, wgs);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 bool prefill_supported(int group) { return group == 2 || group == 4 || group == 8; }
 

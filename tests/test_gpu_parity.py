@@ -543,3 +543,46 @@ def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persis
             start += n_tokens
     finally:
         be_gpu.close()
+
+
+@pytest.mark.parametrize("n_heads,n_kv,wgs", [(20, 5, 0), (20, 5, 1), (20, 5, 3), (20, 5, 37),
+                                              (16, 2, 0), (16, 2, 5), (8, 4, 0), (8, 4, 11)])
+def test_dev_prefill_streamk(monkeypatch, n_heads, n_kv, wgs):
+    """Stream-K prefill (the default tiled launch) with every resident slot
+    (wgs 0) and with few workgroups, so that runs hold many segments and a
+    query tile's key tiles are split over several runs at arbitrary points:
+    queries after cached rows that are not tile-aligned (some segments see no
+    key for their first queries), 2, 4 and 8 query heads per kv head, and two
+    launches in a row (the merge tickets reset themselves)."""
+    case(f"prefill stream-K heads {n_heads}/{n_kv} workgroups {wgs}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_MODE", "2")
+    monkeypatch.setenv("BNR_PREFILL_SK_WGS", str(wgs))
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = 700
+        cache = oracle.KVCache(1, n_kv, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        pre = prefill_workload(44, 45, n_heads, n_kv)
+        oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+        start = 45
+        for n_tokens, s in ((333, 45), (1, 46), (300, 47)):
+            w = prefill_workload(s, n_tokens, n_heads, n_kv)
+            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
+                                                  n_heads=n_heads, n_kv=n_kv)
+            out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+                               n_kv, D, THETA, d_kc, d_vc, cap, out)
+            np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+            assert_close_scaled(host(out), out_ref,
+                                f"stream-K {n_heads}/{n_kv} wgs {wgs} n {n_tokens} start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
