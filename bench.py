@@ -22,6 +22,7 @@ import argparse
 import gc
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -241,6 +242,22 @@ def bench_trait_path(be, steps: int = 300, pos_end: int = 4095):
     return {"rope_us": t_rope / steps * 1e6, "attn_us": t_attn / steps * 1e6,
             "token_layer_us": (t_rope + t_attn) / steps * 1e6, "steps": steps,
             "rms_norm_us": (t1 - t0) / n_glue * 1e6, "sqrelu_gate_us": (t2 - t1) / n_glue * 1e6}
+
+
+def trait_timer(steps: int = 300, pos_end: int = 4095):
+    """The host-slice trait path driven from a compiled caller
+    (bitnetrs_amd/trait_timer, built with the library): what the reference's
+    Rust decode loop would pay per call through an extern "C" block, with no
+    Python between the calls.  None if the program is not built."""
+    exe = os.path.join(ROOT, "bitnetrs_amd", "trait_timer")
+    if not os.path.exists(exe):
+        log("trait_timer is not built; the trait path is timed from Python only")
+        return None
+    res = subprocess.run([exe, str(steps), str(pos_end)], capture_output=True, text=True,
+                         timeout=300)
+    if res.returncode != 0:
+        raise RuntimeError(f"trait_timer failed ({res.returncode}): {res.stderr.strip()}")
+    return json.loads(res.stdout.strip().splitlines()[-1])
 
 
 def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048, n_layers: int = 4):
@@ -745,7 +762,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("decode_kernel", {}).get("bytes_per_launch"),
+                     "traffic": traffic.get("decode_reg_kernel", {}).get("bytes_per_launch"),
                      "kernel": "decode_reg_kernel", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
                      "event_pair_us": round(dec["pair_ms"] * 1e3, 3),
                      "bytes_per_launch": dec["bytes_per_step"],
@@ -755,17 +772,28 @@ def main() -> int:
     }
     if not args.no_trait:
         tp = bench_trait_path(be)
-        log(f"trait path at pos 4095: rope_embed {tp['rope_us']:.1f} us + masked_attention "
-            f"{tp['attn_us']:.1f} us = {tp['token_layer_us']:.1f} us per token and layer; "
-            f"rms_norm {tp['rms_norm_us']:.1f} us, sqrelu_gate {tp['sqrelu_gate_us']:.1f} us")
+        log(f"trait path (Python caller) at pos 4095: rope_embed {tp['rope_us']:.1f} us + "
+            f"masked_attention {tp['attn_us']:.1f} us = {tp['token_layer_us']:.1f} us per token "
+            f"and layer; rms_norm {tp['rms_norm_us']:.1f} us, sqrelu_gate "
+            f"{tp['sqrelu_gate_us']:.1f} us")
+        ct = trait_timer()
+        if ct is not None:
+            log(f"trait path (compiled caller) at pos 4095: rope_embed {ct['rope_us']:.1f} us + "
+                f"masked_attention {ct['attn_us']:.1f} us = {ct['token_layer_us']:.1f} us; "
+                f"rms_norm {ct['rms_norm_us']:.1f} us, sqrelu_gate {ct['sqrelu_gate_us']:.1f} us")
+        main_tp = ct if ct is not None else tp
         line["trait_path"] = {
             "workload": "host_slice_rope_embed_masked_attention_pos4095_hq20_hkv5_d128_fp32",
-            "us_per_token_layer": round(tp["token_layer_us"], 2),
-            "rope_embed_us": round(tp["rope_us"], 2), "masked_attention_us": round(tp["attn_us"], 2),
-            "rms_norm_host_us": round(tp["rms_norm_us"], 2),
-            "sqrelu_gate_host_us": round(tp["sqrelu_gate_us"], 2),
+            "caller": "compiled C over the C ABI (bitnetrs_amd/trait_timer)" if ct is not None
+                      else "Python ctypes (trait_timer not built)",
+            "us_per_token_layer": round(main_tp["token_layer_us"], 2),
+            "rope_embed_us": round(main_tp["rope_us"], 2),
+            "masked_attention_us": round(main_tp["attn_us"], 2),
+            "rms_norm_host_us": round(main_tp["rms_norm_us"], 2),
+            "sqrelu_gate_host_us": round(main_tp["sqrelu_gate_us"], 2),
+            "python_caller_us_per_token_layer": round(tp["token_layer_us"], 2),
             "timed": f"{tp['steps']} consecutive positions after 10 untimed, wall clock per "
-                     "host call (PCIe included), Python GC off"}
+                     "host call (PCIe included); Python caller with its GC off"}
     if not args.no_prefill:
         pre = bench_prefill(torch, be, args.prefill_steps, 2)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, {pre['tflops']:.2f} TFLOP/s; attention "
