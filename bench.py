@@ -737,6 +737,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-tokens", type=int, default=2048,
+                    help="tokens of the single-layer prefill workload (profiling other shapes)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-stack", action="store_true", help="skip the 30-layer stack workload")
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-sequence batched decode")
@@ -823,12 +825,12 @@ def main() -> int:
             "timed": f"{tp['steps']} consecutive positions after 10 untimed, wall clock per "
                      "host call (PCIe included); Python caller with its GC off"}
     if not args.no_prefill:
-        pre = bench_prefill(torch, be, args.prefill_steps, 2)
+        pre = bench_prefill(torch, be, args.prefill_steps, 2, n=args.prefill_tokens)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, {pre['tflops']:.2f} TFLOP/s; attention "
             f"{pre['attn_ms']:.3f} ms, {pre['attn_tflops']:.2f} TFLOP/s (graph); eager event "
             f"pair {pre['pair_ms']:.3f} ms")
         line["prefill"] = {
-            "workload": "gqa_causal_prefill_N2048_hq20_hkv5_d128_fp32",
+            "workload": f"gqa_causal_prefill_N{args.prefill_tokens}_hq20_hkv5_d128_fp32",
             "value": round(pre["tflops"], 3), "unit": "TFLOP/s",
             "ms_per_step": pre["ms_per_step"],
             "roofline": {"bound": "mfma", "achieved": round(pre["attn_tflops"], 3),
