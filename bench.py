@@ -284,6 +284,72 @@ def graph_ms(torch, launch, steps: int, reps: int = 3, restore=None) -> float:
     return best
 
 
+def bench_decode_contexts(torch, be, contexts, steps: int = 200):
+    """Single-sequence fused decode step of the 2B shape at other context
+    lengths: graph-timed over enough rotated layer caches (>= 700 MB in
+    total, at least 8) that the 256 MB MALL cannot hold them."""
+    res = {}
+    for L in contexts:
+        pos, cap = L - 1, L
+        n_layers = max(8, min(64, 700_000_000 // (5120 * L)))
+        g = torch.Generator(device="cuda").manual_seed(0xB17E7021)
+        kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+        vc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+        q = torch.randn(n_layers, HQ * D, device="cuda", generator=g) * 4.0
+        k = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+        v = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+        out = torch.zeros(n_layers, HQ * D, device="cuda")
+
+        def step(i):
+            r = i % n_layers
+            be.dev_decode_step(q[r], k[r], v[r], pos, HQ, HKV, D, THETA, kc[r], vc[r], cap,
+                               out[r])
+
+        for i in range(2 * n_layers):
+            step(i)
+        torch.cuda.synchronize()
+        ms = graph_ms(torch, step, steps)
+        res[L] = {"us_per_step": round(ms * 1e3, 3),
+                  "gbs": round(decode_bytes(L) / (ms * 1e-3) / 1e9, 1),
+                  "frac_hbm": round(decode_bytes(L) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"decode L={L}: {ms * 1e3:.2f} us/step, {res[L]['gbs']:.0f} GB/s")
+        del kc, vc
+        torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill_shapes(torch, be, shapes, steps: int = 10):
+    """Prefill attention (dev_prefill_attention) at other (tokens, cached
+    rows) shapes, graph-timed over 4 rotated layers."""
+    res = {}
+    for n, sp in shapes:
+        cap, nl = n + sp, 4
+        g = torch.Generator(device="cuda").manual_seed(0xB17E7031)
+        q = torch.randn(nl, n, HQ * D, device="cuda", generator=g)
+        kc = torch.randn(nl, HKV, cap, D, device="cuda", generator=g)
+        vc = torch.randn(nl, HKV, cap, D, device="cuda", generator=g)
+        out = torch.zeros(nl, n, HQ * D, device="cuda")
+
+        def attn(i):
+            r = i % nl
+            be.dev_prefill_attention(q[r], kc[r], vc[r], cap, out[r], n, sp, HQ, HKV, D)
+
+        for i in range(2 * nl):
+            attn(i)
+        torch.cuda.synchronize()
+        ms = graph_ms(torch, attn, max(steps, nl))
+        flops = 4 * D * HQ * (n * sp + n * (n + 1) / 2)
+        key = f"{n}@{sp}"
+        res[key] = {"us": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                    "frac_fp32_matrix_peak": round(flops / (ms * 1e-3) / 1e12
+                                                   / FP32_MATRIX_PEAK_TFLOPS, 4)}
+        log(f"prefill attention {n} tokens after {sp}: {ms * 1e3:.1f} us, "
+            f"{res[key]['tflops']:.1f} TFLOP/s")
+        del q, kc, vc, out
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048):
     """2048-token causal prefill of one layer: RoPE + append + attention
     (dev_prefill) and attention alone, each as a HIP graph of one launch per
@@ -737,6 +803,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-contexts", default="",
+                    help="comma-separated context lengths: also time the decode step at each")
+    ap.add_argument("--prefill-shapes", default="",
+                    help="comma-separated tokens@cached shapes: also time prefill attention")
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="tokens of the single-layer prefill workload (profiling other shapes)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -800,6 +870,12 @@ def main() -> int:
                      "stream_floor_gbs": round(dec["bytes_per_step"] / (dec["floor_ms"] * 1e-3) / 1e9, 1),
                      "frac_of_stream_floor": round(dec["floor_ms"] / dec["kernel_ms"], 4)},
     }
+    if args.decode_contexts:
+        line["decode_contexts"] = bench_decode_contexts(
+            torch, be, [int(x) for x in args.decode_contexts.split(",")])
+    if args.prefill_shapes:
+        line["prefill_shapes"] = bench_prefill_shapes(
+            torch, be, [tuple(int(y) for y in x.split("@")) for x in args.prefill_shapes.split(",")])
     if not args.no_trait:
         tp = bench_trait_path(be)
         log(f"trait path (Python caller) at pos 4095: rope_embed {tp['rope_us']:.1f} us + "
