@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) float s_o[NRG][G][D];
   __shared__ float s_m[NRG][G], s_l[NRG][G], s_w[NRG][G], s_M[G], s_L[G], s_R[G];
   __shared__ unsigned long long s_mk[4];
-  __shared__ int s_last;
+  __shared__ int s_last, s_over[W];
 
   const int tid = threadIdx.x;
   const int rg = tid >> 4;
@@ -284,7 +284,14 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g)
     over |= !(mx[g] <= R[g] + kRefSlack) | !(R[g] > -INFINITY && R[g] < INFINITY);
-  const bool exact = __syncthreads_or(over) != 0;
+  // One barrier decides the path: each wave posts whether any of its lanes
+  // needs the exact path (every wave writes its slot, so nothing is cleared).
+  const bool wave_over = __ballot(over) != 0;  // every lane votes
+  if ((tid & 63) == 0) s_over[tid >> 6] = wave_over;
+  __syncthreads();
+  bool exact = false;
+#pragma unroll
+  for (int w = 0; w < W; ++w) exact |= s_over[w] != 0;
 
   const int gs = a.split_off[b] + s;  // global split index
   float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;
