@@ -87,22 +87,26 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
 // (J = w*NI + j); lane l takes row 2J + l/32, LDS chunk l%32.  Rows past the
 // last cached one repeat it (their keys are masked for every query).
 template <int G>
-__device__ __forceinline__ void pf_copy_tile(const PrefillArgs &a, int h, int kt, float *dk,
-                                             float *dv) {
+__device__ __forceinline__ void pf_copy_part(const PrefillArgs &a, int h, int kt, float *dk,
+                                             float *dv, int j) {
   constexpr int NI = kPrefillTile / 4 / (64 * G);  // 1 KB copies per wave per tile
   const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int last_row = a.start_pos + a.n_tokens - 1;
   const float *kc = a.k_cache + h * a.kv_stride;
   const float *vc = a.v_cache + h * a.kv_stride;
+  const int J = wave * NI + j;
+  const int r = 2 * J + hl, p = col;
+  const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
+  dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
+  dma16(vc + grow + 4 * p, dv + J * 256);
+}
+template <int G>
+__device__ __forceinline__ void pf_copy_tile(const PrefillArgs &a, int h, int kt, float *dk,
+                                             float *dv) {
+  constexpr int NI = kPrefillTile / 4 / (64 * G);
 #pragma unroll
-  for (int j = 0; j < NI; ++j) {
-    const int J = wave * NI + j;
-    const int r = 2 * J + hl, p = col;
-    const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
-    dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
-    dma16(vc + grow + 4 * p, dv + J * 256);
-  }
+  for (int j = 0; j < NI; ++j) pf_copy_part<G>(a, h, kt, dk, dv, j);
 }
 
 // This lane's Q fragment (dims 64*hl .. 64*hl+63 of its query, the wave's
@@ -128,6 +132,16 @@ __device__ __forceinline__ void pf_scale_q(float (&qf)[64], float sc) {
   for (int i = 0; i < 64; ++i) qf[i] *= sc;
 }
 
+// max(v of lane l, v of lane l ^ 32), in every lane: one v_permlane32_swap
+// exchanges the two halves of the wave between two copies of v (no LDS
+// round trip, unlike a bpermute); whichever half it moves, the pair's
+// maximum is the same.
+__device__ __forceinline__ float max_half_swap(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
 // S^T tile = K Q^T: 32 keys x 32 queries.
 __device__ __forceinline__ floatx16 pf_tile_s(const float *dk, const float (&qf)[64]) {
   const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
@@ -141,6 +155,34 @@ __device__ __forceinline__ floatx16 pf_tile_s(const float *dk, const float (&qf)
     S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * i + 1], S, 0, 0, 0);
     S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * i + 2], S, 0, 0, 0);
     S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
+  }
+  return S;
+}
+
+// pf_tile_s with the next tile's copies (key tile ktn into nk, nv) issued
+// between its products, and each K row chunk read one group of products
+// ahead of its use; scheduling barriers keep that order.
+template <int G>
+__device__ __forceinline__ floatx16 pf_tile_s_copy(const float *dk, const float (&qf)[64],
+                                                   const PrefillArgs &a, int h, int ktn,
+                                                   float *nk, float *nv) {
+  constexpr int NI = kPrefillTile / 4 / (64 * G);
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  floatx16 S = floatx16{};
+  const float *krow = dk + col * kHeadDim + 64 * hl;
+  const int sw = col & 15;
+  float4 kn = ld4(krow + 4 * sw);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float4 kv = kn;
+    if (i < 15) kn = ld4(krow + 4 * ((i + 1) ^ sw));
+    if (i % (16 / NI) == 1) pf_copy_part<G>(a, h, ktn, nk, nv, i / (16 / NI));
+    __builtin_amdgcn_sched_barrier(0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * i], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * i + 1], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * i + 2], S, 0, 0, 0);
+    S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
   }
   return S;
 }
@@ -162,7 +204,7 @@ __device__ __forceinline__ void pf_tile_pv(const PrefillArgs &a, const PfItem &i
   float mb = S[0];
 #pragma unroll
   for (int r = 1; r < 16; ++r) mb = fmaxf(mb, S[r]);
-  mb = fmaxf(mb, __shfl_xor(mb, 32));
+  mb = max_half_swap(mb);
   // Lazy rescaling: m is the reference the exponentials are taken against;
   // it moves only when a query's max exceeds it by more than 8 (so every
   // p <= 2^8).  O lives in accumulation registers, so a rescale is costly
@@ -281,8 +323,10 @@ void prefill_kernel(PrefillArgs a) {
   // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
   float m = -1e30f, l = 0.f;
   auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv) {
-    if (kt + 1 < it.nkt) pf_copy_tile<G>(a, it.h, kt + 1, nk, nv);
-    const floatx16 S = pf_tile_s(dk, qf);
+    // The next tile's copies go out between this tile's K products (the
+    // last tile copies itself again into the free buffers, so that the copy
+    // needs no branch and shares the products' block).
+    const floatx16 S = pf_tile_s_copy<G>(dk, qf, a, it.h, min(kt + 1, it.nkt - 1), nk, nv);
     pf_tile_pv(a, it, kt, S, dv, O, m, l);
     wait_vmem();  // this wave's copies of the next tile have landed
     __syncthreads();
