@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -215,6 +216,10 @@ struct bnr_ctx {
   float *h_zc = nullptr;  // zero-copy staging: pinned host memory kernels read and write
   float *d_zc = nullptr;  // its device address
   size_t h_zc_n = 0;
+  // Completion words of the host-slice calls: pinned, coherent host memory
+  // the kernels store a call's sequence number into (kSignalWords of them).
+  unsigned *h_sig = nullptr, *d_sig = nullptr;
+  unsigned sig_seq = 0;
 
   // mirrors, most recently used first
   std::list<Mirror> mirrors;
@@ -353,6 +358,49 @@ int ensure_zc(bnr_ctx *c, size_t n) {
 int host_wait(bnr_ctx *c, const char *what) {
   HIP_TRY(hipStreamSynchronize(c->stream), what);
   return BNR_OK;
+}
+
+// Completion words: a host-slice call's kernel stores the call's sequence
+// number into words 0..n-1 (one per workgroup that writes outputs) once its
+// outputs are visible to the host.  The host thread watches them instead of
+// sleeping in a stream synchronisation, whose wake-up costs several
+// microseconds per call.
+constexpr int kSignalWords = 4096;
+
+int ensure_sig(bnr_ctx *c) {
+  if (c->h_sig) return BNR_OK;
+  HIP_TRY(hipHostMalloc((void **)&c->h_sig, kSignalWords * sizeof(unsigned),
+                        hipHostMallocMapped | hipHostMallocCoherent),
+          "completion words alloc");
+  std::memset(c->h_sig, 0, kSignalWords * sizeof(unsigned));
+  hipError_t e = hipHostGetDevicePointer((void **)&c->d_sig, c->h_sig, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(c->h_sig);
+    c->h_sig = c->d_sig = nullptr;
+    return err_hip(e, "completion words map");
+  }
+  return BNR_OK;
+}
+
+// The next call's sequence number (never 0, the words' initial value).
+unsigned next_seq(bnr_ctx *c) {
+  if (++c->sig_seq == 0) c->sig_seq = 1;
+  return c->sig_seq;
+}
+
+// Returns once words 0..n-1 hold seq.  The watch is bounded: after 2 ms
+// (a kernel that faulted never stores) it falls back to synchronising the
+// stream, which also reports any error.
+int host_wait_words(bnr_ctx *c, int n, unsigned seq, const char *what) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (unsigned spins = 0;; ++spins) {
+    int i = 0;
+    while (i < n && __atomic_load_n(&c->h_sig[i], __ATOMIC_ACQUIRE) == seq) ++i;
+    if (i == n) return BNR_OK;
+    if ((spins & 255) == 255 &&
+        std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(2000))
+      return host_wait(c, what);
+  }
 }
 
 // Grow-only, zero-filled ticket counters (kernels leave them zero).
@@ -943,6 +991,7 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     if (c->d_bytes) (void)hipFree(c->d_bytes);
     if (c->h_stage) (void)hipHostFree(c->h_stage);
     if (c->h_zc) (void)hipHostFree(c->h_zc);
+    if (c->h_sig) (void)hipHostFree(c->h_sig);
     float *bufs[] = {c->d_cos, c->d_sin, c->d_q, c->d_out, c->pf_ws};
     for (float *p : bufs)
       if (p) (void)hipFree(p);
@@ -997,8 +1046,16 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
   a.head_dim = (int)hd;
   a.cos_tab = c->d_cos;
   a.sin_tab = c->d_sin;
+  st = ensure_sig(c);
+  if (st) return st;
+  const long long words = rope_append_blocks(a);
+  const bool watch = words <= kSignalWords;
+  if (watch) {
+    a.done = c->d_sig;
+    a.seq = next_seq(c);
+  }
   HIP_TRY(launch_rope_append(a, c->stream), "rope launch");
-  st = host_wait(c, "rope_embed");
+  st = watch ? host_wait_words(c, (int)words, a.seq, "rope_embed") : host_wait(c, "rope_embed");
   if (st) return st;
   if (q_len) std::memcpy(q, h, q_len * sizeof(float));
   if (k_len) std::memcpy(k, h + qs, k_len * sizeof(float));
@@ -1091,10 +1148,16 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     a.v_cache = m->dv;
     a.kv_stride = (long long)(m->rows * head_dim);
     a.out = d + in_n;
+    st = ensure_sig(c);
+    if (st) return st;
+    a.done = c->d_sig;  // set by the reference-merge kernel (the launch checks below)
+    a.seq = next_seq(c);
     const int p = (int)cur_pos;
     st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), m->rows, c->stream);
     if (st) return st;
-    st = host_wait(c, "masked_attention");
+    st = a.merge_ref && a.group <= 4 && (int)n_kv_heads <= kSignalWords
+             ? host_wait_words(c, (int)n_kv_heads, a.seq, "masked_attention")
+             : host_wait(c, "masked_attention");
     if (st) return st;
     std::memcpy(output, h + in_n, out_len * sizeof(float));
     m->synced = seq_len;

@@ -293,6 +293,17 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
 #pragma unroll
   for (int w = 0; w < W; ++w) exact |= s_over[w] != 0;
 
+  // Host-slice calls: the output of (sequence b, kv head h) is in host
+  // memory -- every thread's stores complete, then one release store tells
+  // the waiting host thread.
+  auto signal = [&]() {
+    if (!a.done) return;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+      __hip_atomic_store(a.done + b * a.n_kv + h, a.seq, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+  };
   const int gs = a.split_off[b] + s;  // global split index
   float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;
   if (!exact) {
@@ -310,7 +321,10 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
         add_agent(acc + e, O);
       }
     }
-    if (nsplit == 1) return;
+    if (nsplit == 1) {
+      signal();
+      return;
+    }
     if (tid < G) {
       float Ls = s_l[0][tid];
 #pragma unroll
@@ -378,7 +392,10 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       else
         st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], O);
     }
-    if (nsplit == 1) return;
+    if (nsplit == 1) {
+      signal();
+      return;
+    }
     if (tid < G) {
       float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + tid]);
       st_agent(ml, s_M[tid]);
@@ -407,6 +424,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   if (!s_last) return;
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
+  signal();
 }
 
 template <int G, int W, bool RAGGED>

@@ -44,8 +44,14 @@ struct RopeAppendArgs {
   const float *cos_tab, *sin_tab;  // [table_len x head_dim/2]
   float *k_cache, *v_cache;
   long long kv_stride;  // elements between kv heads of the cache (cap * head_dim)
+  // Host-slice calls: pinned host words; workgroup w stores seq into done[w]
+  // once its outputs are visible to the host (null: no signal).
+  unsigned *done;
+  unsigned seq;
 };
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s);
+// Workgroups of launch_rope_append's launch (the done[] words it sets).
+long long rope_append_blocks(const RopeAppendArgs &a);
 
 // Split-K decode attention for head_dim 128.  One workgroup owns one
 // (sequence, kv head, context chunk) and serves the kv head's G query
@@ -79,6 +85,11 @@ struct DecodeArgs {
   float *acc;
   int ref_waves;  // waves per workgroup of the reference-merge kernel: 4 or 8
   int max_splits;                  // largest split count of the launch (grid x)
+  // Host-slice calls (reference-merge kernel only): pinned host words; the
+  // workgroup that writes the output of (sequence b, kv head h) stores seq
+  // into done[b * n_kv + h] once that output is visible to the host.
+  unsigned *done;
+  unsigned seq;
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
 };

@@ -59,6 +59,12 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
       dst[i + half] = src[i + half];
     }
   }
+  if (a.done) {  // every thread's stores complete, then one release store to the host
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.done + blockIdx.x, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // Four consecutive pairs (i .. i+3, i+half .. i+half+3) per thread, 16-byte
@@ -97,6 +103,12 @@ __global__ __launch_bounds__(256) void rope_append_vec_kernel(RopeAppendArgs a) 
       st4(dst + i, ld4(src + i));
       st4(dst + i + half, ld4(src + i + half));
     }
+  }
+  if (a.done) {  // every thread's stores complete, then one release store to the host
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_store(a.done + blockIdx.x, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 
@@ -705,16 +717,27 @@ hipError_t launch_decode_g(const DecodeArgs &a, hipStream_t s) {
 }
 }  // namespace
 
-hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s) {
+namespace {
+bool rope_append_vec(const RopeAppendArgs &a) {
   auto a16 = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
   const int half = a.head_dim / 2;
-  const bool vec = half % 4 == 0 && a16(a.q) && a16(a.k) && a16(a.cos_tab) && a16(a.sin_tab) &&
-                   (!a.v_cache || (a16(a.v) && a16(a.v_cache))) && (!a.k_cache || a16(a.k_cache)) &&
-                   a.kv_stride % 4 == 0;
-  const long long total = (long long)a.n_tokens * (a.n_heads + 2 * a.n_kv) * (vec ? half / 4 : half);
-  if (total == 0) return hipSuccess;
-  long long blocks = (total + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
+  return half % 4 == 0 && a16(a.q) && a16(a.k) && a16(a.cos_tab) && a16(a.sin_tab) &&
+         (!a.v_cache || (a16(a.v) && a16(a.v_cache))) && (!a.k_cache || a16(a.k_cache)) &&
+         a.kv_stride % 4 == 0;
+}
+}  // namespace
+
+long long rope_append_blocks(const RopeAppendArgs &a) {
+  const int half = a.head_dim / 2;
+  const long long total =
+      (long long)a.n_tokens * (a.n_heads + 2 * a.n_kv) * (rope_append_vec(a) ? half / 4 : half);
+  return std::min<long long>((total + 255) / 256, 65536);
+}
+
+hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s) {
+  const bool vec = rope_append_vec(a);
+  const long long blocks = rope_append_blocks(a);
+  if (blocks == 0) return hipSuccess;
   if (vec)
     rope_append_vec_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(a);
   else
