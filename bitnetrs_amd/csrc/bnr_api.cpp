@@ -2036,8 +2036,11 @@ int check_rms_norm(size_t in_len, size_t w_len, float eps, size_t out_len) {
 
 int run_norm_quant(bnr_ctx *c, int mode, const float *a, const float *b, const float *gamma,
                    float eps, size_t n, float *h_out, float *y_out, int8_t *q_out,
-                   float *scale_out, float *act_absmax, hipStream_t s) {
+                   float *scale_out, float *act_absmax, hipStream_t s, unsigned *done = nullptr,
+                   unsigned seq = 0) {
   NormQuantArgs na{};
+  na.done = done;
+  na.seq = seq;
   na.mode = mode;
   na.a = a;
   na.b = b;
@@ -2073,10 +2076,13 @@ extern "C" int bnr_rms_norm(bnr_ctx *c, const float *input, size_t in_len, const
   st = ensure_zc(c, is + in_len);
   if (st) return st;
   std::memcpy(c->h_zc, input, in_len * sizeof(float));
-  st = run_norm_quant(c, kGluePlain, c->d_zc, nullptr, (const float *)dw, eps, in_len, nullptr,
-                      c->d_zc + is, nullptr, nullptr, nullptr, c->stream);
+  st = ensure_sig(c);
   if (st) return st;
-  st = host_wait(c, "rms_norm");
+  const unsigned seq = next_seq(c);
+  st = run_norm_quant(c, kGluePlain, c->d_zc, nullptr, (const float *)dw, eps, in_len, nullptr,
+                      c->d_zc + is, nullptr, nullptr, nullptr, c->stream, c->d_sig, seq);
+  if (st) return st;
+  st = host_wait_words(c, 1, seq, "rms_norm");
   if (st) return st;
   std::memcpy(output, c->h_zc + is, in_len * sizeof(float));
   return set_ok();
@@ -2099,8 +2105,15 @@ extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, cons
   float *h = c->h_zc, *d = c->d_zc;
   std::memcpy(h, gate, g_len * sizeof(float));
   std::memcpy(h + gs, up, g_len * sizeof(float));
-  HIP_TRY(launch_sqrelu(d, d + gs, d + 2 * gs, (long long)g_len, c->stream), "sqrelu launch");
-  st = host_wait(c, "sqrelu_gate");
+  st = ensure_sig(c);
+  if (st) return st;
+  const long long words = sqrelu_blocks((long long)g_len);
+  const unsigned seq = next_seq(c);
+  HIP_TRY(launch_sqrelu(d, d + gs, d + 2 * gs, (long long)g_len, c->stream,
+                        words <= kSignalWords ? c->d_sig : nullptr, seq),
+          "sqrelu launch");
+  st = words <= kSignalWords ? host_wait_words(c, (int)words, seq, "sqrelu_gate")
+                             : host_wait(c, "sqrelu_gate");
   if (st) return st;
   std::memcpy(out, h + 2 * gs, g_len * sizeof(float));
   return set_ok();

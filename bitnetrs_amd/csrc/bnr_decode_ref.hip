@@ -297,12 +297,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   // memory -- every thread's stores complete, then one release store tells
   // the waiting host thread.
   auto signal = [&]() {
-    if (!a.done) return;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0)
-      __hip_atomic_store(a.done + b * a.n_kv + h, a.seq, __ATOMIC_RELEASE,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
+    if (a.done) signal_host(a.done + b * a.n_kv + h, a.seq);
   };
   const int gs = a.split_off[b] + s;  // global split index
   float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;

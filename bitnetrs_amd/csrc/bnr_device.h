@@ -116,6 +116,15 @@ __device__ __forceinline__ float ld_agent(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Host-slice calls: every thread's stores complete, then thread 0 stores seq
+// into a pinned host word with a system-scope release, so the workgroup's
+// outputs reach the host before the word does.  All threads must call it.
+__device__ __forceinline__ void signal_host(unsigned *word, unsigned seq) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(word, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Device-scope float add whose result is not used: one global_atomic_add_f32
 // (device memory is coarse-grained; the library is built with
 // -munsafe-fp-atomics so that this is not a compare-and-swap loop).

@@ -15,6 +15,7 @@
 // agrees with the reference to rounding; given y, q and the scales are
 // computed exactly as the reference does (one f32 multiply, round half away
 // from zero, correctly rounded division and square root).
+#include "bnr_device.h"
 #include "bnr_internal.h"
 
 #include <hip/hip_runtime.h>
@@ -128,7 +129,10 @@ __global__ __launch_bounds__(kNormLanes) void norm_quant_kernel(NormQuantArgs a)
       if (a.y_out) a.y_out[i] = y;
       mx = fmaxf(mx, fabsf(y));
     }
-  if (!a.q_out) return;
+  if (!a.q_out) {
+    if (a.done) signal_host(a.done, a.seq);
+    return;
+  }
   const float m = fmaxf(block_max(mx, red), 1e-5f);  // f32::max(max_abs, ABSMAX_MIN)
   const float scale = m / 127.0f;
   const float inv_scale = 127.0f / m;
@@ -147,16 +151,18 @@ __global__ __launch_bounds__(kNormLanes) void norm_quant_kernel(NormQuantArgs a)
       if (a.gamma) y = glue_y(y, inv, a.gamma[i]);
       a.q_out[i] = (int8_t)fminf(fmaxf(roundf(y * inv_scale), -128.0f), 127.0f);
     }
+  if (a.done) signal_host(a.done, a.seq);
 }
 
 // out = (max(gate,0)^2) * up, elementwise (CpuBackend::sqrelu_gate).
 __global__ __launch_bounds__(256) void sqrelu_kernel(const float *gate, const float *up, float *out,
-                                                     long long n) {
+                                                     long long n, unsigned *done, unsigned seq) {
 #pragma clang fp contract(off)
   for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
     const float r = fmaxf(gate[i], 0.0f);
     out[i] = r * r * up[i];
   }
+  if (done) signal_host(done + blockIdx.x, seq);
 }
 
 // h += delta (axpy_f32_fast(1.0, delta, h): one rounding per element).
@@ -173,10 +179,11 @@ hipError_t launch_norm_quant(const NormQuantArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_sqrelu(const float *gate, const float *up, float *out, long long n, hipStream_t s) {
+hipError_t launch_sqrelu(const float *gate, const float *up, float *out, long long n, hipStream_t s,
+                         unsigned *done, unsigned seq) {
   if (n <= 0) return hipSuccess;
-  const long long blocks = std::min<long long>((n + 255) / 256, 4096);
-  sqrelu_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(gate, up, out, n);
+  const long long blocks = sqrelu_blocks(n);
+  sqrelu_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(gate, up, out, n, done, seq);
   return hipGetLastError();
 }
 

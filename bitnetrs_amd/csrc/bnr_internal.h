@@ -403,9 +403,18 @@ struct NormQuantArgs {
   int8_t *q_out;        // optional: absmax int8 quantisation of y
   float *scale_out;     // optional (with q_out): max|y| / 127
   float *act_absmax;    // optional (with q_out): scale * 127, what the projections take
+  unsigned *done;       // host-slice calls: pinned host word set to seq at the end (or null)
+  unsigned seq;
 };
 hipError_t launch_norm_quant(const NormQuantArgs &a, hipStream_t s);
-hipError_t launch_sqrelu(const float *gate, const float *up, float *out, long long n, hipStream_t s);
+// done (host-slice calls): workgroup w stores seq into done[w] at its end;
+// sqrelu_blocks(n) workgroups.
+hipError_t launch_sqrelu(const float *gate, const float *up, float *out, long long n, hipStream_t s,
+                         unsigned *done = nullptr, unsigned seq = 0);
+inline long long sqrelu_blocks(long long n) {
+  const long long b = (n + 255) / 256;
+  return b < 4096 ? b : 4096;
+}
 hipError_t launch_residual(float *h, const float *delta, long long n, hipStream_t s);
 
 }  // namespace bnr

@@ -59,12 +59,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendArgs a) {
       dst[i + half] = src[i + half];
     }
   }
-  if (a.done) {  // every thread's stores complete, then one release store to the host
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_store(a.done + blockIdx.x, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
+  if (a.done) signal_host(a.done + blockIdx.x, a.seq);
 }
 
 // Four consecutive pairs (i .. i+3, i+half .. i+half+3) per thread, 16-byte
@@ -104,12 +99,7 @@ __global__ __launch_bounds__(256) void rope_append_vec_kernel(RopeAppendArgs a) 
       st4(dst + i + half, ld4(src + i + half));
     }
   }
-  if (a.done) {  // every thread's stores complete, then one release store to the host
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_store(a.done + blockIdx.x, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
+  if (a.done) signal_host(a.done + blockIdx.x, a.seq);
 }
 
 // Merge the nsplit partial states of (sequence b, kv head h) into the
