@@ -367,19 +367,24 @@ int host_wait(bnr_ctx *c, const char *what) {
 // microseconds per call.
 constexpr int kSignalWords = 4096;
 
-int ensure_sig(bnr_ctx *c) {
-  if (c->h_sig) return BNR_OK;
-  HIP_TRY(hipHostMalloc((void **)&c->h_sig, kSignalWords * sizeof(unsigned),
-                        hipHostMallocMapped | hipHostMallocCoherent),
-          "completion words alloc");
+// False when pinned, mapped memory cannot be had: the calls then wait with a
+// stream synchronisation instead.
+bool ensure_sig(bnr_ctx *c) {
+  if (c->h_sig) return true;
+  if (hipHostMalloc((void **)&c->h_sig, kSignalWords * sizeof(unsigned),
+                    hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
+    c->h_sig = nullptr;
+    (void)hipGetLastError();
+    return false;
+  }
   std::memset(c->h_sig, 0, kSignalWords * sizeof(unsigned));
-  hipError_t e = hipHostGetDevicePointer((void **)&c->d_sig, c->h_sig, 0);
-  if (e != hipSuccess) {
+  if (hipHostGetDevicePointer((void **)&c->d_sig, c->h_sig, 0) != hipSuccess) {
     (void)hipHostFree(c->h_sig);
     c->h_sig = c->d_sig = nullptr;
-    return err_hip(e, "completion words map");
+    (void)hipGetLastError();
+    return false;
   }
-  return BNR_OK;
+  return true;
 }
 
 // The next call's sequence number (never 0, the words' initial value).
@@ -1046,10 +1051,8 @@ extern "C" int bnr_rope_embed(bnr_ctx *c, float *q, size_t q_len, float *k, size
   a.head_dim = (int)hd;
   a.cos_tab = c->d_cos;
   a.sin_tab = c->d_sin;
-  st = ensure_sig(c);
-  if (st) return st;
   const long long words = rope_append_blocks(a);
-  const bool watch = words <= kSignalWords;
+  const bool watch = words <= kSignalWords && ensure_sig(c);
   if (watch) {
     a.done = c->d_sig;
     a.seq = next_seq(c);
@@ -1148,14 +1151,15 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     a.v_cache = m->dv;
     a.kv_stride = (long long)(m->rows * head_dim);
     a.out = d + in_n;
-    st = ensure_sig(c);
-    if (st) return st;
-    a.done = c->d_sig;  // set by the reference-merge kernel (the launch checks below)
-    a.seq = next_seq(c);
+    const bool sig = (int)n_kv_heads <= kSignalWords && ensure_sig(c);
+    if (sig) {
+      a.done = c->d_sig;  // set by the reference-merge kernel (the launch checks below)
+      a.seq = next_seq(c);
+    }
     const int p = (int)cur_pos;
     st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), m->rows, c->stream);
     if (st) return st;
-    st = a.merge_ref && a.group <= 4 && (int)n_kv_heads <= kSignalWords
+    st = sig && a.merge_ref && a.group <= 4
              ? host_wait_words(c, (int)n_kv_heads, a.seq, "masked_attention")
              : host_wait(c, "masked_attention");
     if (st) return st;
@@ -2076,13 +2080,13 @@ extern "C" int bnr_rms_norm(bnr_ctx *c, const float *input, size_t in_len, const
   st = ensure_zc(c, is + in_len);
   if (st) return st;
   std::memcpy(c->h_zc, input, in_len * sizeof(float));
-  st = ensure_sig(c);
-  if (st) return st;
-  const unsigned seq = next_seq(c);
+  const bool sig = ensure_sig(c);
+  const unsigned seq = sig ? next_seq(c) : 0;
   st = run_norm_quant(c, kGluePlain, c->d_zc, nullptr, (const float *)dw, eps, in_len, nullptr,
-                      c->d_zc + is, nullptr, nullptr, nullptr, c->stream, c->d_sig, seq);
+                      c->d_zc + is, nullptr, nullptr, nullptr, c->stream, sig ? c->d_sig : nullptr,
+                      seq);
   if (st) return st;
-  st = host_wait_words(c, 1, seq, "rms_norm");
+  st = sig ? host_wait_words(c, 1, seq, "rms_norm") : host_wait(c, "rms_norm");
   if (st) return st;
   std::memcpy(output, c->h_zc + is, in_len * sizeof(float));
   return set_ok();
@@ -2105,15 +2109,13 @@ extern "C" int bnr_sqrelu_gate(bnr_ctx *c, const float *gate, size_t g_len, cons
   float *h = c->h_zc, *d = c->d_zc;
   std::memcpy(h, gate, g_len * sizeof(float));
   std::memcpy(h + gs, up, g_len * sizeof(float));
-  st = ensure_sig(c);
-  if (st) return st;
   const long long words = sqrelu_blocks((long long)g_len);
-  const unsigned seq = next_seq(c);
+  const bool sig = words <= kSignalWords && ensure_sig(c);
+  const unsigned seq = sig ? next_seq(c) : 0;
   HIP_TRY(launch_sqrelu(d, d + gs, d + 2 * gs, (long long)g_len, c->stream,
-                        words <= kSignalWords ? c->d_sig : nullptr, seq),
+                        sig ? c->d_sig : nullptr, seq),
           "sqrelu launch");
-  st = words <= kSignalWords ? host_wait_words(c, (int)words, seq, "sqrelu_gate")
-                             : host_wait(c, "sqrelu_gate");
+  st = sig ? host_wait_words(c, (int)words, seq, "sqrelu_gate") : host_wait(c, "sqrelu_gate");
   if (st) return st;
   std::memcpy(out, h + 2 * gs, g_len * sizeof(float));
   return set_ok();
