@@ -900,6 +900,12 @@ def main() -> int:
             "python_caller_us_per_token_layer": round(tp["token_layer_us"], 2),
             "timed": f"{tp['steps']} consecutive positions after 10 untimed, wall clock per "
                      "host call (PCIe included); Python caller with its GC off"}
+        if ct is not None and "kv_decode_us" in ct:
+            # bnr_kv_decode: the same token and layer through the backend-owned
+            # cache (rope_embed, store_kv and masked_attention in one call)
+            line["trait_path"]["owned_cache_kv_decode_us"] = round(ct["kv_decode_us"], 2)
+            log(f"owned-cache decode (bnr_kv_decode, compiled caller) at pos 4095: "
+                f"{ct['kv_decode_us']:.1f} us per token and layer")
     if not args.no_prefill:
         pre = bench_prefill(torch, be, args.prefill_steps, 2, n=args.prefill_tokens)
         log(f"prefill: {pre['ms_per_step']:.3f} ms/step, {pre['tflops']:.2f} TFLOP/s; attention "

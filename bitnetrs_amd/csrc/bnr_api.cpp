@@ -1533,10 +1533,14 @@ extern "C" int bnr_dev_decode_attention_noalloc(bnr_ctx *c, const float *q, cons
 namespace {
 
 // bnr_dev_decode_step after validation; the caller holds c->mu.
+// done/seq (host-slice calls): completion words for the reference-merge
+// kernel; *signals tells whether the launch stores them.
 int decode_step_locked(bnr_ctx *c, const float *q, const float *k, const float *v,
                        size_t position, size_t n_heads, size_t n_kv_heads, size_t head_dim,
                        float theta, float *k_cache, float *v_cache, size_t cap, float *out,
-                       float *q_rot, float *k_rot, hipStream_t s) {
+                       float *q_rot, float *k_rot, hipStream_t s, unsigned *done = nullptr,
+                       unsigned seq = 0, bool *signals = nullptr) {
+  if (signals) *signals = false;
   DeviceGuard dg(c->device);
   // The table covers every row of the cache (no rebuild on later calls).
   int st = ensure_table(c, std::max(position + 1, cap) - 1, head_dim, theta);
@@ -1557,8 +1561,11 @@ int decode_step_locked(bnr_ctx *c, const float *q, const float *k, const float *
     a.k_rot = k_rot;
     a.cos_tab = c->d_cos;
     a.sin_tab = c->d_sin;
+    a.done = done;
+    a.seq = seq;
     const int p = (int)position;
     st = run_decode(c, a, &p, 1, (int)n_kv_heads, (int)(n_heads / n_kv_heads), cap, s);
+    if (!st && signals) *signals = done && a.merge_ref && a.group <= 4;
     return st ? st : set_ok();
   }
   // Any other shape: rotate copies, append, then the generic kernel.
@@ -2360,29 +2367,33 @@ extern "C" int bnr_kv_decode(bnr_ctx *c, bnr_kv_cache *kc, size_t layer, float *
   if (kc->device != c->device) return err_backend("kv cache and context are on different devices");
   std::lock_guard<std::mutex> lc(c->mu);
   DeviceGuard dg(c->device);
-  // Staging, one pinned copy each way: [q | k | v] in, then [out | rotated q
-  // | rotated k] back, every part 16-byte aligned.
+  // Zero-copy staging, [q | k | v | out | rotated q | rotated k], every part
+  // 16-byte aligned: the decode kernel reads its inputs from pinned host
+  // memory and writes its outputs there, and the call waits for its
+  // completion words (a stream synchronisation where the kernel stores none).
   const size_t qs = round4(q_len), ks = round4(kvn), os = round4(out_len);
   const size_t in_n = qs + 2 * ks, back_n = os + qs + ks;
-  st = ensure_buf(&c->d_q, &c->d_q_n, in_n + back_n, "staging alloc");
+  st = ensure_zc(c, in_n + back_n);
   if (st) return st;
-  st = ensure_host(c, std::max(in_n, back_n));
-  if (st) return st;
-  float *h = c->h_stage;
+  float *h = c->h_zc;
   std::memcpy(h, q, q_len * sizeof(float));
   std::memcpy(h + qs, k, kvn * sizeof(float));
   std::memcpy(h + qs + ks, v, kvn * sizeof(float));
-  float *dq = c->d_q, *dk = dq + qs, *dv = dk + ks, *dout = dq + in_n, *dqr = dout + os,
+  float *dq = c->d_zc, *dk = dq + qs, *dv = dk + ks, *dout = dq + in_n, *dqr = dout + os,
         *dkr = dqr + qs;
-  HIP_TRY(hipMemcpyAsync(dq, h, in_n * 4, hipMemcpyHostToDevice, c->stream), "upload q/k/v");
+  const bool sig = (int)nkv <= kSignalWords && ensure_sig(c);
+  const unsigned seq = sig ? next_seq(c) : 0;
+  bool signals = false;
   st = decode_step_locked(c, dq, dk, dv, position, n_heads, nkv, hd, theta, kc->k(layer),
-                          kc->v(layer), kc->max_seq, dout, dqr, dkr, c->stream);
+                          kc->v(layer), kc->max_seq, dout, dqr, dkr, c->stream,
+                          sig ? c->d_sig : nullptr, seq, &signals);
   if (st) return st;
-  HIP_TRY(hipMemcpyAsync(h, dout, back_n * 4, hipMemcpyDeviceToHost, c->stream), "download");
-  HIP_TRY(hipStreamSynchronize(c->stream), "kv_decode");
-  std::memcpy(output, h, out_len * sizeof(float));
-  std::memcpy(q, h + os, q_len * sizeof(float));
-  std::memcpy(k, h + os + qs, kvn * sizeof(float));
+  st = signals ? host_wait_words(c, (int)nkv, seq, "kv_decode") : host_wait(c, "kv_decode");
+  if (st) return st;
+  const float *hb = h + in_n;
+  std::memcpy(output, hb, out_len * sizeof(float));
+  std::memcpy(q, hb + os, q_len * sizeof(float));
+  std::memcpy(k, hb + os + qs, kvn * sizeof(float));
   kv_mark_stored(kc, layer, position, 1);
   return set_ok();
 }

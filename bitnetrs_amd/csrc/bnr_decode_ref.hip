@@ -409,6 +409,11 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   if (tid < G) s_R[tid] = R[tid];
   __syncthreads();
+  // Host-slice calls: split 0's rotated q and k (in host memory) reach the
+  // host before its ticket, hence before the merging workgroup's completion
+  // word (a system-scope release: this XCD's L2 is written back).
+  if (a.done && s == 0 && tid == 0 && (a.q_rot || a.k_rot))
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
   unsigned *ctr = a.counters + (b * a.n_kv + h) * kCounterStride;
   if (tid == 0) {
     const unsigned ticket =

@@ -6,7 +6,10 @@
  * bnr_rope_embed, the store of the new k/v row into the host cache, then
  * bnr_masked_attention at positions pos_end-steps+1 .. pos_end, after 10
  * untimed ones; then bnr_rms_norm (2560) and bnr_sqrelu_gate (6912) host
- * calls.  Prints one JSON object.  Used by bench.py; needs a GPU.
+ * calls; then the backend-owned cache's one-call decode (bnr_kv_decode:
+ * rope_embed, store_kv and masked_attention of a token and layer) at the same
+ * positions, after the cache is filled up to them.  Prints one JSON object.
+ * Used by bench.py; needs a GPU.
  *
  * usage: trait_timer [steps] [pos_end]
  */
@@ -114,11 +117,27 @@ int main(int argc, char **argv) {
   for (int i = 0; i < n_glue; ++i)
     if (bnr_sqrelu_gate(c, gate, FFN, up, FFN, inner, FFN)) return die("sqrelu_gate");
   const double g2 = now_us();
+  /* backend-owned cache, one layer: fill rows 0 .. p0-1, then time the
+   * one-call decode at p0 .. pos_end (KVCache::advance after each token) */
+  bnr_kv_cache *kvc = NULL;
+  if (bnr_kv_cache_create(c, 1, HKV, D, CAP, &kvc)) return die("kv_cache_create");
+  double t_kv = 0;
+  for (int pos = 0; pos <= pos_end; ++pos) {
+    memcpy(q, q0, sizeof q);
+    memcpy(k, k0, sizeof k);
+    const double t0 = now_us();
+    if (bnr_kv_decode(c, kvc, 0, q, HQ * D, k, HKV * D, v0, HKV * D, pos, HQ, theta, out, HQ * D))
+      return die("kv_decode");
+    const double t1 = now_us();
+    if (bnr_kv_cache_advance(kvc, 1)) return die("kv_cache_advance");
+    if (pos >= p0) t_kv += t1 - t0;
+  }
+  bnr_kv_cache_destroy(kvc);
   printf("{\"steps\": %d, \"pos_end\": %d, \"rope_us\": %.3f, \"attn_us\": %.3f, "
          "\"token_layer_us\": %.3f, \"rms_norm_us\": %.3f, \"sqrelu_gate_us\": %.3f, "
-         "\"out0\": %.6g}\n",
+         "\"kv_decode_us\": %.3f, \"out0\": %.6g}\n",
          steps, pos_end, t_rope / steps, t_attn / steps, (t_rope + t_attn) / steps,
-         (g1 - g0) / n_glue, (g2 - g1) / n_glue, (double)out[0]);
+         (g1 - g0) / n_glue, (g2 - g1) / n_glue, t_kv / steps, (double)out[0]);
   bnr_destroy(c);
   free(kc);
   free(vc);
