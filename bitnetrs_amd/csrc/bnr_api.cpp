@@ -236,7 +236,7 @@ struct bnr_ctx {
   int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel ticket; 2: reference merge
   int split_cost = -1;  // planner cost of a split of the in-kernel merges (ns); -1: mode default
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
-  int ref_waves = 8;    // reference merge: waves per workgroup of small launches (4 or 8)
+  int ref_waves = 0;    // reference merge, small launches: 4 or 8 waves, 0: by length
 
   // device scratch of bnr_dev_decode_attention_noalloc (this GPU's copy)
   void *noalloc = nullptr;
@@ -734,10 +734,14 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
       rows = std::max(lo, 16);
     }
     rows = std::max(rows, (max_len + kMaxSplits - 1) / kMaxSplits);
-    // Small launches run 8-wave workgroups (one per CU) with up to 3 rows
-    // per row group and pass; large ones 4-wave workgroups (two resident per
-    // CU) with up to 4 (graph-timed sweeps on MI355X, contexts 512-32768).
-    a.ref_waves = large || c->ref_waves == 4 ? 4 : 8;
+    // Small launches run one workgroup per CU: 8 waves with up to 3 rows per
+    // row group and pass, or 4 waves with up to 6 for sequences of at most
+    // kRefWaves4Rows rows; large ones 4-wave workgroups (two resident per CU)
+    // with up to 4 (graph-timed sweeps on MI355X, contexts 512-32768).
+    const int small_waves = c->ref_waves == 4 || c->ref_waves == 8
+                                ? c->ref_waves
+                                : (max_len <= kRefWaves4Rows ? 4 : 8);
+    a.ref_waves = large ? 4 : small_waves;
     const int nrg = 4 * a.ref_waves;  // row groups of 16 lanes
     const int rpg_max = large ? 4 : a.ref_waves == 8 ? 3 : 6;
     const int r = c->force_rpg ? std::min(c->force_rpg, 6) : std::min(rpg_max, (rows + nrg - 1) / nrg);

@@ -122,9 +122,14 @@ struct DecodePlanConfig {
   int merge_mode;  // -1: reference merge (default); 0: second kernel; 1: in-kernel ticket; 2: reference merge
   int split_cost;  // planner cost of one split of the in-kernel merges (ns), -1: the mode's default
   int ref_rows;    // reference merge: rows per split (0: planner decides)
-  int ref_waves;   // reference merge, small launches: 4 waves per workgroup if 4, else 8
-                   // (large launches: 4)
+  int ref_waves;   // reference merge, small launches: 4 or 8 waves per workgroup, or 0:
+                   // 4 up to kRefWaves4Rows rows, 8 beyond (large launches: 4)
 };
+// Small reference-merge launches of at most this many rows per sequence run
+// 4-wave workgroups (graph-timed on MI355X, 2B shape: 4 waves 5.98 vs 6.30 us
+// at 512 rows, 7.33 vs 7.48 us at 1536; 8 waves 7.42 vs 7.57 us at 2048 and
+// 8.98 vs 9.23 us at 4096).
+constexpr int kRefWaves4Rows = 1792;
 // Split-K plan of one decode launch over sequences of lens[b] rows: fills
 // a.rpg, a.passes, a.rows_per_split, a.batch, a.split_off, a.max_splits and
 // a.merge_inline.

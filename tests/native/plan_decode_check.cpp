@@ -2,14 +2,15 @@
 // against libbitnet_hip.so; no GPU is touched.  Prints "ok" or the first
 // violated property.
 //
-// Properties, over 9900 seeded launches (1..64 sequences, 1..8192 rows,
+// Properties, over 10800 seeded launches (1..64 sequences, 1..8192 rows,
 // 1..64 kv heads, the default 256-CU configuration and tuning overrides):
 //  - every plan: 1 <= rpg <= 8, passes >= 1, the split counts are
 //    ceil(len_b / rows_per_split), max_splits is the largest (at most
 //    kMaxSplits);
 //  - reference merge (the default): rows_per_split fits its passes of
-//    4*waves*rpg rows (8 waves and rpg <= 3 for small launches, or 4 waves
-//    and rpg <= 6 when configured; 4 waves and rpg <= 4 for large
+//    4*waves*rpg rows (small launches: 8 waves and rpg <= 3, or 4 waves and
+//    rpg <= 6 -- configured, or by default for sequences of at most
+//    kRefWaves4Rows rows; 4 waves and rpg <= 4 for large
 //    launches), at least 16 rows; the launch fits its target (one workgroup
 //    per CU, eight for large launches) whenever one split per (sequence,
 //    kv head) does, and no smaller split size would fit it;
@@ -67,7 +68,9 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
   if (c.merge_mode < 0 || c.merge_mode == 2) {
     if (!a.merge_ref || !a.merge_inline) return fail("reference merge chosen", L0, batch, n_kv);
     if (rows < 16) return fail("at least 16 rows", L0, batch, n_kv);
-    const int waves = large || c.ref_waves == 4 ? 4 : 8;
+    const int small_waves =
+        c.ref_waves == 4 || c.ref_waves == 8 ? c.ref_waves : (max_len <= kRefWaves4Rows ? 4 : 8);
+    const int waves = large ? 4 : small_waves;
     const int nrg = 4 * waves;  // row groups of a workgroup
     if (a.ref_waves != waves) return fail("reference waves", L0, batch, n_kv);
     if (!(nrg * a.rpg * (a.passes - 1) < rows && rows <= nrg * a.rpg * a.passes))
@@ -129,11 +132,11 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
 }
 
 int main() {
-  const DecodePlanConfig def{256, 256, 1024, 0, 1, -1, -1, 0, 8};
+  const DecodePlanConfig def{256, 256, 1024, 0, 1, -1, -1, 0, 0};
   const DecodePlanConfig ticket{256, 256, 1024, 0, 1, 1, -1, 0, 8};
   // The 2B shape, one sequence: the plans of both merges.
   struct Want { int L, rpg, passes, rows; };
-  const Want want_ref[] = {{512, 1, 1, 32},   {2048, 2, 1, 64},  {4096, 3, 1, 96},
+  const Want want_ref[] = {{512, 1, 1, 16},   {2048, 2, 1, 64},  {4096, 3, 1, 96},
                            {8192, 3, 2, 192}, {32768, 3, 7, 672}};
   for (const Want &w : want_ref) {
     DecodeArgs a{};
@@ -163,6 +166,7 @@ int main() {
                                    {256, 256, 1024, 0, 1, -1, -1, 200, 4}, // forced split size
                                    {128, 128, 512, 0, 1, -1, -1, 0, 4},    // a smaller device
                                    {256, 256, 1024, 0, 1, -1, -1, 0, 4},   // four waves
+                                   {256, 256, 1024, 0, 1, -1, -1, 0, 8},   // eight waves
                                    ticket,
                                    {256, 256, 1024, 0, 2, 1, -1, 0, 4},    // ticket, at least two passes
                                    {256, 128, 1024, 0, 1, 1, -1, 0, 4},    // ticket, a smaller target

@@ -4,7 +4,7 @@ split whose workgroups fit the launch's target; for the forced ticket and
 two-launch merges the two-launch merge only where its kernels exist and
 small launches at the cheapest split by the planner's time estimate; the
 plans of the 2B shape.  A host-only harness is built with hipcc against the
-library and run over 9900 seeded launches (no GPU needed)."""
+library and run over 10800 seeded launches (no GPU needed)."""
 import os
 import shutil
 import subprocess
