@@ -142,7 +142,7 @@ void fingerprint(const uint8_t *p, size_t len, uint8_t *out) {
 constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
-  int n_tokens, start_pos, n_kv, tiles;
+  int n_tokens, start_pos, n_kv, tiles, balanced;
 };
 
 struct DeviceGuard {
@@ -247,6 +247,7 @@ struct bnr_ctx {
   int pf_chunk_tiles = -1;  // -1: planner decides; else key tiles per chunk
   int pf_mode = kPrefillAuto;  // tiled prefill launch: kPrefillAuto / Grid / Queue / StreamK
   int pf_sk_wgs = 0;              // stream-K workgroups (0: every resident slot)
+  int pf_balanced = -1;           // balanced key chunks: -1 planner, 0 never, 1 always
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
 
@@ -466,11 +467,12 @@ DecodeWs &ws_for(bnr_ctx *c, hipStream_t s) { return s == c->stream ? c->hws : c
 // a fixed cost (queries and first tile loaded, outputs stored), plus a
 // partial-state store when its query tile is split; the last chunk of a
 // split tile then reads the others' partials.  The items come in the
-// kernel's order (prefill_map).  The constants are fitted to measured
+// kernel's order (prefill_map, or pf_bal_map for balanced chunks).  The constants are fitted to measured
 // MI355X spans over 15 shapes x 6 chunk sizes (128 to 8192 tokens, start
 // 0 to 4000; a tile of 4 heads alone on a CU takes about 4 us): they keep
 // the chosen chunk size within 10 % of the best measured one (2 % median).
-double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu) {
+double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu,
+                    bool balanced) {
   constexpr double kShared = 1.9, kFixed = 1.0, kStore = 0.0, kMerge = 0.1;
   constexpr int kXcd = 8, kSlots = 2;
   const int ncu = std::max(1, n_cu / kXcd);
@@ -521,17 +523,24 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
   order.start_pos = start_pos;
   order.n_qtiles = (n_tokens + 31) / 32;
   order.chunk_tiles = std::min(std::max(ctiles_in, 1), kPrefillNoSplit);
+  order.balanced = balanced;
   prefill_order(order);
   const int ctiles = order.chunk_tiles;
   const int n_items = prefill_plan(n_tokens, start_pos, ctiles).n_items;
   double now = 0.0, span = 0.0;
   long long wg = 0;
   for (int y = 0; y < n_items; ++y) {
-    int qt, ch, nch, base;
-    prefill_map(order, y, qt, ch, nch, base);
-    const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
+    int qt, ch, nch, base, t;
+    if (order.balanced) {
+      pf_bal_map(order, y, qt, ch, nch);
+      int kt0;
+      pf_bal_range(std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1, nch, ch, kt0, t);
+    } else {
+      prefill_map(order, y, qt, ch, nch, base);
+      const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
+      t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
+    }
     {
-      const int t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
       for (int h = 0; h < n_kv; ++h, ++wg) {
         if (wg % kXcd != 0) continue;
         int cu;
@@ -581,31 +590,40 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
   return span;
 }
 
-// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split); the
-// last 16 shapes are remembered, a new one costs a replay per candidate
-// (tens to hundreds of us each).  Sizes between the powers of two matter:
+// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split), and
+// whether the chunks are balanced (*balanced); the last 16 shapes are
+// remembered, a new one costs two replays per candidate (tens to hundreds
+// of us each).  Sizes between the powers of two matter:
 // they set how evenly the items fill the resident slots (N = 1024 runs 8 %
 // faster at 6 tiles than at 4, 512 queries after 1536 cached 14 % faster at
 // 10 than at 4 or 16).
 constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
 constexpr long long kPrefillMaxSplitItems = 8192;  // (kv head, item) pairs of a planned split
 
-int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv) {
+int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv, int *balanced) {
   for (const PrefillPlanEntry &e : c->pf_plans)
-    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) return e.tiles;
-  int best = kPrefillNoSplit;
-  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, c->n_cu);
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) {
+      *balanced = e.balanced;
+      return e.tiles;
+    }
+  int best = kPrefillNoSplit, best_bal = 0;
+  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, c->n_cu, false);
   for (int ct : kPrefillChunkCandidates) {
     if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > kPrefillMaxSplitItems)
       continue;
-    const double span = prefill_span(n_tokens, start_pos, n_kv, ct, c->n_cu);
-    if (span < best_span * 0.99) {
-      best_span = span;
-      best = ct;
+    for (int bal = 0; bal <= 1; ++bal) {
+      if ((bal == 0 && c->pf_balanced == 1) || (bal == 1 && c->pf_balanced == 0)) continue;
+      const double span = prefill_span(n_tokens, start_pos, n_kv, ct, c->n_cu, bal != 0);
+      if (span < best_span * 0.99) {
+        best_span = span;
+        best = ct;
+        best_bal = bal;
+      }
     }
   }
   if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
-  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, best});
+  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, best, best_bal});
+  *balanced = best_bal;
   return best;
 }
 
@@ -980,6 +998,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT"))
     if (atoi(v) > 0) c->pf_mode = kPrefillQueue;
   if (const char *v = std::getenv("BNR_PREFILL_SK_WGS")) c->pf_sk_wgs = std::max(atoi(v), 0);
+  if (const char *v = std::getenv("BNR_PREFILL_BALANCED")) c->pf_balanced = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_MODE")) {
     const int m = atoi(v);
     if (m >= kPrefillGrid && m <= kPrefillAuto) c->pf_mode = m;
@@ -1707,9 +1726,11 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
                          (c->pf_mode == kPrefillStreamK ||
                           (c->pf_mode == kPrefillAuto && start_pos >= n_tokens));
     if (!streamk) {
+      int bal = c->pf_balanced == 1;
       pa.chunk_tiles = c->pf_chunk_tiles > 0
                            ? c->pf_chunk_tiles
-                           : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads);
+                           : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads, &bal);
+      pa.balanced = bal;
     } else {
       pa.chunk_tiles = kPrefillNoSplit;
     }

@@ -178,6 +178,13 @@ struct PrefillArgs {
   // of one tile consecutive.
   int lpt, n_full;
   int part_off[64];
+  // Balanced key chunks (balanced = 1, chunk_tiles <= kMaxLptChunk): a query
+  // tile of nk key tiles keeps its nch = ceil(nk / chunk_tiles) chunks, but
+  // they take nk / nch tiles each, the first nk % nch one more, and the
+  // items go longest first (pf_bal_map).  bal_off[l] = items longer than l
+  // key tiles (prefill_order fills it).
+  int balanced;
+  int bal_off[65];
   // Stream-K launch (sk_units > 0): units = (kv head, query tile, key tile)
   // tile products in that order, sk_per_head of them per kv head; the
   // launch's workgroups take equal runs of them.  ws then holds two partial
@@ -277,6 +284,85 @@ __host__ __device__ inline void prefill_map(const PrefillArgs &a, int y, int &qt
   base = (int)(pf_ceil_sum(qt - 1 + A, ct) - pf_ceil_sum(A - 1, ct));
 }
 
+// Key tiles kt0 .. kt0 + len - 1 of chunk ch of a query tile with nk key
+// tiles cut into nch balanced chunks.
+__host__ __device__ inline void pf_bal_range(int nk, int nch, int ch, int &kt0, int &len) {
+  const int q = nk / nch, r = nk - q * nch;
+  kt0 = ch * q + (ch < r ? ch : r);
+  len = q + (ch < r ? 1 : 0);
+}
+
+// Work item y (per kv head) of a balanced launch -> query tile qt, chunk ch
+// of its nch chunks.  Order: chunk length descending; within one length the
+// last query tile first, then the others from the highest down; within a
+// tile, chunks in order.  A query tile qt < nqt-1 has nk = A + qt key tiles
+// (A as in prefill_map) and nch = m = ceil(nk / ct) chunks: with q = nk / m
+// and r = nk % m, chunks 0 .. r-1 have q + 1 tiles and r .. m-1 have q.  So
+// the tiles of block m (nch = m) with a chunk of length l are those with
+// q = l (nk in [l m, l m + m - 1], its m - r chunks ch = r ..) and those
+// with q = l - 1 (nk in [(l-1) m + 1, l m - 1], its r chunks ch = 0 ..): a
+// block's count is two arithmetic sums, and only the block that holds item
+// y is walked tile by tile.  The host's dispatch replay and the kernels use
+// this same function.
+__host__ __device__ inline void pf_bal_map(const PrefillArgs &a, int y, int &qt, int &ch,
+                                           int &nch) {
+  const int ct = a.chunk_tiles, nqt = a.n_qtiles;
+  const int A = (a.start_pos + 31) / 32 + 1;
+  const int nk_last = (a.start_pos + a.n_tokens - 1) / 32 + 1;
+  int l = ct;
+  while (l > 1 && y >= a.bal_off[l - 1]) --l;
+  long long k = y - a.bal_off[l];
+  {
+    const int m = (nk_last + ct - 1) / ct, q = nk_last / m, r = nk_last - q * m;
+    const int c = l == q + 1 ? r : (l == q ? m - r : 0);
+    if (k < c) {
+      qt = nqt - 1;
+      nch = m;
+      ch = (l == q + 1 ? 0 : r) + (int)k;
+      return;
+    }
+    k -= c;
+  }
+  const int nk_hi = A + nqt - 2;  // the highest regular tile (none if nqt == 1)
+  for (int m = (nk_hi + ct - 1) / ct; nqt > 1 && m >= 1; --m) {
+    const int lo = (m - 1) * ct + 1 > A ? (m - 1) * ct + 1 : A;
+    const int hi = m * ct < nk_hi ? m * ct : nk_hi;
+    if (lo > hi) break;  // blocks below hold no regular tile
+    const int a1 = lo > l * m ? lo : l * m, b1 = hi < l * m + m - 1 ? hi : l * m + m - 1;
+    const int a2 = lo > (l - 1) * m + 1 ? lo : (l - 1) * m + 1, b2 = hi < l * m - 1 ? hi : l * m - 1;
+    const long long n1 = b1 >= a1 ? b1 - a1 + 1 : 0, n2 = b2 >= a2 ? b2 - a2 + 1 : 0;
+    const long long s1 = n1 * ((long long)m + (long long)l * m) - (a1 + (long long)b1) * n1 / 2;
+    const long long s2 = (a2 + (long long)b2) * n2 / 2 - n2 * (long long)(l - 1) * m;
+    if (k >= s1 + s2) {
+      k -= s1 + s2;
+      continue;
+    }
+    for (int nk = b1; nk >= a1; --nk) {  // q == l: m - r chunks of length l
+      const int r = nk - l * m;
+      if (k < m - r) {
+        qt = nk - A;
+        nch = m;
+        ch = r + (int)k;
+        return;
+      }
+      k -= m - r;
+    }
+    for (int nk = b2; nk >= a2; --nk) {  // q == l - 1: r chunks of length l
+      const int r = nk - (l - 1) * m;
+      if (k < r) {
+        qt = nk - A;
+        nch = m;
+        ch = (int)k;
+        return;
+      }
+      k -= r;
+    }
+  }
+  qt = 0;  // not reached for y below the item count
+  ch = 0;
+  nch = 1;
+}
+
 // (query tile, chunk) items per kv head of a prefill launch, and the key
 // tiles they cover in total.
 struct PrefillPlan {
@@ -285,8 +371,10 @@ struct PrefillPlan {
   bool split;  // some query tile has more than one chunk
 };
 PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_tiles);
-// Fills a.lpt, a.n_full and a.part_off from a.n_tokens, a.start_pos,
-// a.n_qtiles and a.chunk_tiles.
+// Fills a.lpt, a.n_full and a.part_off (and a.bal_off when a.balanced)
+// from a.n_tokens, a.start_pos, a.n_qtiles and a.chunk_tiles.  Balanced
+// chunks need 1 < chunk_tiles <= kMaxLptChunk; otherwise a.balanced is
+// cleared.
 void prefill_order(PrefillArgs &a);
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.
 // Stream-K runs: workgroup w of P takes units [sk_u0(w), sk_u0(w + 1)), a

@@ -75,6 +75,16 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
   it.h = h;
   it.y = y;
   const int last_row = a.start_pos + a.n_tokens - 1;
+  if (a.balanced) {
+    pf_bal_map(a, y, it.qt, it.ch, it.nch);
+    const int A = (a.start_pos + 31) / 32 + 1;
+    it.base = (int)(pf_ceil_sum(it.qt - 1 + A, a.chunk_tiles) - pf_ceil_sum(A - 1, a.chunk_tiles));
+    it.q0 = it.qt * 32;
+    int len;
+    pf_bal_range(min(a.start_pos + it.q0 + 31, last_row) / 32 + 1, it.nch, it.ch, it.kt0, len);
+    it.nkt = it.kt0 + len;
+    return it;
+  }
   prefill_map(a, y, it.qt, it.ch, it.nch, it.base);
   it.q0 = it.qt * 32;
   const int kmax = min(a.start_pos + it.q0 + 31, last_row);
@@ -651,7 +661,24 @@ void prefill_order(PrefillArgs &a) {
   a.lpt = ct <= kMaxLptChunk && ct > 1;
   a.n_full = 0;
   for (int b = 0; b < kMaxLptChunk; ++b) a.part_off[b] = 0;
-  if (!a.lpt) return;
+  for (int l = 0; l <= kMaxLptChunk; ++l) a.bal_off[l] = 0;
+  if (!a.lpt) {
+    a.balanced = 0;
+    return;
+  }
+  if (a.balanced) {
+    // chunks per length: a tile of nk key tiles in m chunks has nk % m of
+    // length nk / m + 1 (at most ct) and the others of nk / m
+    long long cnt[kMaxLptChunk + 2] = {};
+    auto add = [&](int nk) {
+      const int m = (nk + ct - 1) / ct, q = nk / m, r = nk - q * m;
+      cnt[q + 1] += r;
+      cnt[q] += m - r;
+    };
+    add(nt_last);
+    for (int qt = 0; qt + 1 < nqt; ++qt) add(qt + A);
+    for (int l = ct; l >= 1; --l) a.bal_off[l - 1] = a.bal_off[l] + (int)cnt[l];
+  }
   int count[kMaxLptChunk] = {};  // last chunks of length r (< ct)
   a.n_full = nt_last / ct;
   count[nt_last % ct] += 1;

@@ -545,6 +545,52 @@ def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persis
         be_gpu.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv,tiles,persistent", [(20, 5, 2, 0), (20, 5, 3, 0), (20, 5, 5, 0),
+                                                           (20, 5, 7, 0), (20, 5, 3, 1), (20, 5, 6, 1),
+                                                           (16, 2, 3, 0), (16, 2, 5, 1), (8, 4, 4, 0),
+                                                           (8, 4, 3, 1)])
+def test_dev_prefill_balanced_chunks(monkeypatch, n_heads, n_kv, tiles, persistent):
+    """Balanced key chunks (a query tile's chunks differ by at most one key
+    tile, dispatched longest first): queries after cached rows that are not
+    tile-aligned, 2, 4 and 8 query heads per kv head, grid and persistent
+    launches, and two launches in a row (the merge tickets reset
+    themselves)."""
+    case(f"prefill balanced chunks heads {n_heads}/{n_kv} tiles {tiles} persistent {persistent}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_CHUNK_TILES", str(tiles))
+    monkeypatch.setenv("BNR_PREFILL_BALANCED", "1")
+    monkeypatch.setenv("BNR_PREFILL_PERSISTENT", str(persistent))
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = 640
+        cache = oracle.KVCache(1, n_kv, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        pre = prefill_workload(46, 45, n_heads, n_kv)
+        oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+        start = 45
+        for n_tokens, s in ((300, 47), (129, 48)):
+            w = prefill_workload(s, n_tokens, n_heads, n_kv)
+            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
+                                                  n_heads=n_heads, n_kv=n_kv)
+            out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+                               n_kv, D, THETA, d_kc, d_vc, cap, out)
+            np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+            assert_close(host(out), out_ref,
+                         f"prefill balanced {n_heads}/{n_kv} chunks of {tiles} n {n_tokens} "
+                         f"start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
+
+
 @pytest.mark.parametrize("n_heads,n_kv,wgs", [(20, 5, 0), (20, 5, 1), (20, 5, 3), (20, 5, 37),
                                               (16, 2, 0), (16, 2, 5), (8, 4, 0), (8, 4, 11)])
 def test_dev_prefill_streamk(monkeypatch, n_heads, n_kv, wgs):
