@@ -260,13 +260,19 @@ def trait_timer(steps: int = 300, pos_end: int = 4095):
     return json.loads(res.stdout.strip().splitlines()[-1])
 
 
-def graph_ms(torch, launch, steps: int, reps: int = 3, restore=None) -> float:
+def graph_ms(torch, launch, steps: int, reps: int = 3, restore=None, warm: int = 3) -> float:
     """Per-launch time of `steps` launches captured in one HIP graph: the
-    fastest of `reps` replays, each after `restore()` (untimed) when given."""
+    fastest of `reps` replays, each after `restore()` (untimed) when given,
+    after `warm` untimed replays (a short graph's first replays after the
+    host-side setup run below the part's steady clock)."""
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(steps):
             launch(i)
+    for _ in range(warm):
+        if restore is not None:
+            restore()
+        graph.replay()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     best = None
