@@ -754,14 +754,18 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
     rows = std::max(rows, (max_len + kMaxSplits - 1) / kMaxSplits);
     // Small launches run one workgroup per CU: 8 waves with up to 3 rows per
     // row group and pass, or 4 waves with up to 6 for sequences of at most
-    // kRefWaves4Rows rows; large ones 4-wave workgroups (two resident per CU)
-    // with up to 4 (graph-timed sweeps on MI355X, contexts 512-32768).
+    // kRefWaves4Rows rows (graph-timed sweeps on MI355X, contexts
+    // 512-32768).  Large ones run 4-wave workgroups with up to 3 rows per
+    // row group while a split takes at most kLargeRpg3Rows rows (5 passes;
+    // three workgroups resident per CU) and up to 4 beyond (two per CU, fewer
+    // passes): 16-40 sequences of U[128, 4096) rows measured 3-11 % faster at
+    // 3, 48 and 64 sequences 2-10 % slower.
     const int small_waves = c->ref_waves == 4 || c->ref_waves == 8
                                 ? c->ref_waves
                                 : (max_len <= kRefWaves4Rows ? 4 : 8);
     a.ref_waves = large ? 4 : small_waves;
     const int nrg = 4 * a.ref_waves;  // row groups of 16 lanes
-    const int rpg_max = large ? 4 : a.ref_waves == 8 ? 3 : 6;
+    const int rpg_max = large ? (rows <= kLargeRpg3Rows ? 3 : 4) : a.ref_waves == 8 ? 3 : 6;
     const int r = c->force_rpg ? std::min(c->force_rpg, 6) : std::min(rpg_max, (rows + nrg - 1) / nrg);
     a.rpg = r;
     a.passes = (rows + nrg * r - 1) / (nrg * r);

@@ -130,6 +130,10 @@ struct DecodePlanConfig {
 // at 512 rows, 7.33 vs 7.48 us at 1536; 8 waves 7.42 vs 7.57 us at 2048 and
 // 8.98 vs 9.23 us at 4096).
 constexpr int kRefWaves4Rows = 1792;
+// Large reference-merge launches: splits of at most this many rows use at
+// most 3 rows per row group and pass (5 passes of a 4-wave workgroup), longer
+// ones up to 4.
+constexpr int kLargeRpg3Rows = 240;
 // Split-K plan of one decode launch over sequences of lens[b] rows: fills
 // a.rpg, a.passes, a.rows_per_split, a.batch, a.split_off, a.max_splits and
 // a.merge_inline.

@@ -10,7 +10,8 @@
 //  - reference merge (the default): rows_per_split fits its passes of
 //    4*waves*rpg rows (small launches: 8 waves and rpg <= 3, or 4 waves and
 //    rpg <= 6 -- configured, or by default for sequences of at most
-//    kRefWaves4Rows rows; 4 waves and rpg <= 4 for large
+//    kRefWaves4Rows rows; 4 waves and rpg <= 3 (splits of at most
+//    kLargeRpg3Rows rows) or 4 for large
 //    launches), at least 16 rows; the launch fits its target (one workgroup
 //    per CU, eight for large launches) whenever one split per (sequence,
 //    kv head) does, and no smaller split size would fit it;
@@ -90,6 +91,12 @@ static int check(const DecodePlanConfig &c, const int *lens, int batch, int n_kv
       }
       const int r0 = smallest;
       const int rpg = a.rpg;
+      // large launches: at most 3 rows per row group up to kLargeRpg3Rows rows
+      if (large && c.force_rpg == 0) {
+        const int cap = r0 <= kLargeRpg3Rows ? 3 : 4;
+        const int want = (r0 + nrg - 1) / nrg < cap ? (r0 + nrg - 1) / nrg : cap;
+        if (rpg != want) return fail("large reference rpg", L0, batch, n_kv);
+      }
       // the plan is the smallest fitting size rounded up to whole passes
       const int passes = (r0 + nrg * rpg - 1) / (nrg * rpg);
       if (rows != nrg * rpg * passes && rows != r0)
