@@ -31,29 +31,52 @@ BNR_GLUE_SQRELU = 2
 
 
 class BitNetError(Exception):
-    """Mirror of bitnet_core::error::BitNetError (bitnet-core/src/error.rs:12-55)."""
+    """Mirror of bitnet_core::error::BitNetError (bitnet-core/src/error.rs:12-55).
+
+    ``fields`` holds the variant's own fields as the library reports them
+    (``bnr_last_error_parts``); ``str()`` is the variant's Display text,
+    rebuilt from them.
+    """
 
     kind = -1
+    FORMAT = "{0}"
+
+    def __init__(self, *fields: str):
+        self.fields = fields
+        super().__init__(self.FORMAT.format(*fields))
 
 
 class InvalidShape(BitNetError):
     kind = BNR_INVALID_SHAPE
+    FORMAT = "invalid tensor shape: expected {0}, got {1}"
+
+    @property
+    def expected(self) -> str:
+        return self.fields[0]
+
+    @property
+    def got(self) -> str:
+        return self.fields[1]
 
 
 class InvalidConfig(BitNetError):
     kind = BNR_INVALID_CONFIG
+    FORMAT = "invalid model configuration: {0}"
 
 
 class BackendError(BitNetError):
     kind = BNR_BACKEND_ERROR
+    FORMAT = "backend error ({0}): {1}"
 
 
 class UnsupportedDevice(BitNetError):
     kind = BNR_UNSUPPORTED_DEVICE
+    FORMAT = "unsupported device: {0}"
 
 
 class QuantizationError(BitNetError):
     kind = BNR_QUANTIZATION_ERROR
+    FORMAT = "quantization error: {0}"
 
 
 ERRORS = {
@@ -81,6 +104,7 @@ _i32p = _c.POINTER(_c.c_int32)
 # name -> (restype, argtypes); one entry per function in include/bitnet_hip.h
 SIGNATURES = {
     "bnr_last_error": (_c.c_char_p, []),
+    "bnr_last_error_parts": (_c.c_int, [_c.POINTER(_c.c_char_p), _c.POINTER(_c.c_char_p)]),
     "bnr_abi_version": (_c.c_uint32, []),
     "bnr_create": (_c.c_int, [_c.c_int, _c.POINTER(_vp)]),
     "bnr_destroy": (None, [_vp]),
@@ -174,8 +198,26 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+# Fields each variant takes from bnr_last_error_parts (first, second).
+_N_FIELDS = {BNR_INVALID_SHAPE: 2, BNR_BACKEND_ERROR: 2}
+
+
+def last_error() -> BitNetError:
+    """The calling thread's last error, rebuilt from its fields."""
+    lib = load()
+    first, second = _c.c_char_p(), _c.c_char_p()
+    kind = lib.bnr_last_error_parts(_c.byref(first), _c.byref(second))
+    parts = [(first.value or b"").decode(), (second.value or b"").decode()]
+    cls = ERRORS.get(kind)
+    if cls is None:
+        return BitNetError(lib.bnr_last_error().decode())
+    return cls(*parts[:_N_FIELDS.get(kind, 1)])
+
+
 def check(status: int) -> None:
     """Raise the BitNetError subclass for a non-zero status."""
     if status != BNR_OK:
-        msg = load().bnr_last_error().decode()
-        raise ERRORS.get(status, BitNetError)(msg)
+        err = last_error()
+        if err.kind != status:  # cannot happen: the library records every failure
+            raise BitNetError(f"status {status} with last error {err!s}")
+        raise err

@@ -327,19 +327,18 @@ class DeviceKVCache:
         """store_kv's position rules (lib.rs:209-216) for n_tokens rows from position."""
         last = position + n_tokens - 1
         if last >= self.max_seq:
-            raise InvalidShape(f"invalid tensor shape: expected position < max_seq "
-                               f"({self.max_seq}), got position = {last}")
+            raise InvalidShape(f"position < max_seq ({self.max_seq})", f"position = {last}")
         if position > self.layer_lengths[layer]:
-            raise InvalidShape(f"invalid tensor shape: expected position <= layer_len_positions "
-                               f"({self.layer_lengths[layer]}), got position = {position}")
+            raise InvalidShape(f"position <= layer_len_positions ({self.layer_lengths[layer]})",
+                               f"position = {position}")
 
     def mark_stored(self, layer: int, position: int, n_tokens: int = 1) -> None:
         self.layer_lengths[layer] = max(self.layer_lengths[layer], position + n_tokens)
 
     def advance(self, n: int = 1) -> None:
         if self.filled_positions + n > self.max_seq:
-            raise BackendError(f"KVCache::advance overflow: filled_positions="
-                               f"{self.filled_positions} max_seq={self.max_seq}")
+            raise BackendError("HIP", f"KVCache::advance overflow: filled_positions="
+                                      f"{self.filled_positions} max_seq={self.max_seq}")
         self.filled_positions += n
 
     def clear(self) -> None:

@@ -27,19 +27,39 @@
 using namespace bnr;
 
 // ---------------------------------------------------------------------------
-// Errors: thread-local message, text as BitNetError's Display
-// (bitnet-core/src/error.rs:12-55).
+// Errors: the calling thread's last error, kept both as BitNetError's Display
+// text and as the fields of its variant (bitnet-core/src/error.rs:12-55), so
+// that a binding can rebuild the variant itself:
+//   InvalidShape { expected, got }       first = expected, second = got
+//   InvalidConfig(String)                first = the message
+//   BackendError { backend, message }    first = "HIP", second = the message
+//   UnsupportedDevice(String)            first = the message
+//   QuantizationError(String)            first = the message
 // ---------------------------------------------------------------------------
-static thread_local std::string g_err;
+namespace {
+struct LastError {
+  int kind = BNR_OK;
+  std::string text, first, second;
+};
+}  // namespace
+static thread_local LastError g_err;
+
+static int set_err(int kind, std::string text, std::string first, std::string second) {
+  g_err.kind = kind;
+  g_err.text = std::move(text);
+  g_err.first = std::move(first);
+  g_err.second = std::move(second);
+  return kind;
+}
 
 static int set_ok() {
-  g_err.clear();
+  g_err = LastError();
   return BNR_OK;
 }
 
 static int err_shape(const std::string &expected, const std::string &got) {
-  g_err = "invalid tensor shape: expected " + expected + ", got " + got;
-  return BNR_INVALID_SHAPE;
+  return set_err(BNR_INVALID_SHAPE, "invalid tensor shape: expected " + expected + ", got " + got,
+                 expected, got);
 }
 
 static std::string fmt(const char *f, ...) {
@@ -52,18 +72,19 @@ static std::string fmt(const char *f, ...) {
 }
 
 static int err_config(const std::string &msg) {
-  g_err = "invalid model configuration: " + msg;
-  return BNR_INVALID_CONFIG;
+  return set_err(BNR_INVALID_CONFIG, "invalid model configuration: " + msg, msg, "");
 }
 
 static int err_backend(const std::string &msg) {
-  g_err = "backend error (HIP): " + msg;
-  return BNR_BACKEND_ERROR;
+  return set_err(BNR_BACKEND_ERROR, "backend error (HIP): " + msg, "HIP", msg);
 }
 
 static int err_quant(const std::string &msg) {
-  g_err = "quantization error: " + msg;
-  return BNR_QUANTIZATION_ERROR;
+  return set_err(BNR_QUANTIZATION_ERROR, "quantization error: " + msg, msg, "");
+}
+
+static int err_device(const std::string &msg) {
+  return set_err(BNR_UNSUPPORTED_DEVICE, "unsupported device: " + msg, msg, "");
 }
 
 // Rust's Display of an f32: the shortest decimal that reads back to the same
@@ -939,9 +960,15 @@ Mirror *find_mirror(bnr_ctx *c, const float *hk, size_t k_len, const float *hv, 
 // ---------------------------------------------------------------------------
 // Lifecycle
 // ---------------------------------------------------------------------------
-extern "C" const char *bnr_last_error(void) { return g_err.c_str(); }
+extern "C" const char *bnr_last_error(void) { return g_err.text.c_str(); }
 
-extern "C" uint32_t bnr_abi_version(void) { return (1u << 16) | 1u; }
+extern "C" int bnr_last_error_parts(const char **first, const char **second) {
+  if (first) *first = g_err.first.c_str();
+  if (second) *second = g_err.second.c_str();
+  return g_err.kind;
+}
+
+extern "C" uint32_t bnr_abi_version(void) { return (1u << 16) | 2u; }
 
 extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (!out) return err_backend("bnr_create: out is NULL");
@@ -949,19 +976,16 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   int n = 0;
   hipError_t e = hipGetDeviceCount(&n);
   if (e != hipSuccess || n == 0) {
-    g_err = "unsupported device: no HIP device available";
-    return BNR_UNSUPPORTED_DEVICE;
+    return err_device("no HIP device available");
   }
   if (device_id < 0 || device_id >= n) {
-    g_err = fmt("unsupported device: HIP device %d does not exist (%d present)", device_id, n);
-    return BNR_UNSUPPORTED_DEVICE;
+    return err_device(fmt("HIP device %d does not exist (%d present)", device_id, n));
   }
   hipDeviceProp_t prop;
   HIP_TRY(hipGetDeviceProperties(&prop, device_id), "hipGetDeviceProperties");
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-    g_err = fmt("unsupported device: HIP device %d is %s, this library is built for gfx950",
-                device_id, prop.gcnArchName);
-    return BNR_UNSUPPORTED_DEVICE;
+    return err_device(fmt("HIP device %d is %s, this library is built for gfx950", device_id,
+                          prop.gcnArchName));
   }
   DeviceGuard dg(device_id);
   bnr_ctx *c = new bnr_ctx();

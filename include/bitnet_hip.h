@@ -47,6 +47,21 @@ typedef struct bnr_ctx bnr_ctx;
 /* Message of the last failed call on this thread ("" after a success). */
 const char *bnr_last_error(void);
 
+/* The same error as fields, so that a binding rebuilds the BitNetError
+ * variant itself rather than wrapping the Display text again
+ * (bitnet-core/src/error.rs:12-55).  Returns the status of the error that
+ * bnr_last_error() describes (BNR_OK when there is none) and points *first
+ * and *second (either may be NULL) at:
+ *   BNR_INVALID_SHAPE       expected, got     InvalidShape { expected, got }
+ *   BNR_INVALID_CONFIG      message, ""       InvalidConfig(message)
+ *   BNR_BACKEND_ERROR       "HIP", message    BackendError { backend, message }
+ *   BNR_UNSUPPORTED_DEVICE  message, ""       UnsupportedDevice(message)
+ *   BNR_QUANTIZATION_ERROR  message, ""       QuantizationError(message)
+ * Display of the variant built from them equals bnr_last_error().  The
+ * strings belong to the calling thread and stay valid until its next call
+ * into the library. */
+int bnr_last_error_parts(const char **first, const char **second);
+
 /* ABI version of this header: (major << 16) | minor. */
 uint32_t bnr_abi_version(void);
 

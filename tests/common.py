@@ -24,6 +24,41 @@ SCALE_REL = 1e-4
 HQ, HKV, D, THETA = 20, 5, 128, 500000.0
 
 
+# BitNetError's Display format of each variant the path returns
+# (bitnet-core/src/error.rs:17-55), by the library's status code.
+RUST_DISPLAY = {
+    1: "invalid tensor shape: expected {0}, got {1}",  # InvalidShape { expected, got }
+    2: "invalid model configuration: {0}",  # InvalidConfig(String)
+    3: "backend error ({0}): {1}",  # BackendError { backend, message }
+    4: "unsupported device: {0}",  # UnsupportedDevice(String)
+    5: "quantization error: {0}",  # QuantizationError(String)
+}
+
+
+def error_from_parts() -> tuple:
+    """(status, Display) of the calling thread's last library error, the
+    Display rebuilt from bnr_last_error_parts' fields with the Rust format
+    string -- what a binding that constructs the variant prints.  Checks that
+    a one-field variant leaves the second field empty and that the rebuilt
+    text equals bnr_last_error()."""
+    import ctypes
+
+    from bitnetrs_amd import _lib
+
+    lib = _lib.load()
+    first, second = ctypes.c_char_p(), ctypes.c_char_p()
+    kind = lib.bnr_last_error_parts(ctypes.byref(first), ctypes.byref(second))
+    a, b = first.value.decode(), second.value.decode()
+    if kind == 0:
+        return 0, ""
+    if kind not in (1, 3):
+        assert b == "", (kind, a, b)
+    assert a != "", (kind, a, b)
+    text = RUST_DISPLAY[kind].format(a, b)
+    assert text == lib.bnr_last_error().decode(), (text, lib.bnr_last_error())
+    return kind, text
+
+
 def seed(cfg: int, tensor_id: int) -> int:
     """Seed of tensor `tensor_id` of workload `cfg`: 0xB17E7000 + 16*cfg + id."""
     return 0xB17E7000 + 16 * cfg + tensor_id

@@ -10,6 +10,7 @@ import pytest
 
 import bitnetrs_amd
 from bitnetrs_amd import _lib
+from common import error_from_parts
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -55,9 +56,30 @@ def test_abi_version_and_no_device_error():
         has_gpu = False
     if has_gpu:
         pytest.skip("a GPU is present")
-    with pytest.raises(bitnetrs_amd.UnsupportedDevice):
+    with pytest.raises(bitnetrs_amd.UnsupportedDevice) as e:
         bitnetrs_amd.HipBackend(0)
     assert "device" in lib.bnr_last_error().decode()
+    assert error_from_parts() == (_lib.BNR_UNSUPPORTED_DEVICE,
+                                  "unsupported device: no HIP device available")
+    assert e.value.fields == ("no HIP device available",)
+    assert str(e.value) == lib.bnr_last_error().decode()
+
+
+def test_error_parts_rebuild_each_variant_without_gpu():
+    """bnr_last_error_parts gives each variant's fields: a binding that builds
+    the variant from them prints bnr_last_error()'s text exactly."""
+    lib = _lib.load()
+    assert lib.bnr_create(0, None) == _lib.BNR_BACKEND_ERROR
+    assert error_from_parts() == (_lib.BNR_BACKEND_ERROR,
+                                  "backend error (HIP): bnr_create: out is NULL")
+    assert lib.bnr_rope_embed(None, None, 0, None, 0, 0, 8, 1, 1, 1e4) == _lib.BNR_BACKEND_ERROR
+    kind, text = error_from_parts()
+    assert kind == _lib.BNR_BACKEND_ERROR and text.startswith("backend error (HIP): ")
+    with pytest.raises(bitnetrs_amd.BackendError) as e:
+        _lib.check(lib.bnr_rope_embed(None, None, 0, None, 0, 0, 8, 1, 1, 1e4))
+    assert e.value.fields[0] == "HIP" and str(e.value) == text
+    # null out-pointers are allowed; the status is still returned
+    assert lib.bnr_last_error_parts(None, None) == _lib.BNR_BACKEND_ERROR
 
 
 def test_null_context_is_an_error_not_a_crash():

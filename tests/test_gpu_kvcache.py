@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 
 import oracle
-from common import (D, HKV, HQ, THETA, assert_close, oracle_prefill, prefill_workload, seed)
+from common import (D, HKV, HQ, THETA, assert_close, error_from_parts, oracle_prefill, prefill_workload,
+                    seed)
 
 pytestmark = pytest.mark.gpu
 f32 = np.float32
@@ -123,6 +124,7 @@ def test_native_cache_errors_match_oracle(backend):
             kc.decode(layer, q.copy(), k.copy(), v, pos, HQ, theta, np.zeros(HQ * D, f32))
         except bitnetrs_amd.BitNetError as e:
             got = (type(e).__name__, str(e))
+            assert error_from_parts() == (e.kind, str(e))
         try:
             qr, kr = q.copy(), k.copy()
             be.rope_embed(qr, kr, pos, D, HQ, HKV, theta)
@@ -155,6 +157,8 @@ def test_native_cache_errors_match_oracle(backend):
             ref.advance()
         with pytest.raises(bitnetrs_amd.BackendError) as e:
             kc.advance()
+        assert error_from_parts() == (e.value.kind, str(e.value))
+        assert e.value.fields[0] == "HIP"
         with pytest.raises(Exception) as e_ref:
             ref.advance()
         assert str(e.value) == f"backend error (HIP): {e_ref.value}" or \

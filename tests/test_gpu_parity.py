@@ -14,6 +14,7 @@ import pytest
 
 import oracle
 from common import (D, HKV, HQ, THETA, assert_close, assert_close_scaled, batched_lengths,
+                    error_from_parts,
                     decode_workload, oracle_decode, oracle_prefill, prefill_workload, seed)
 
 pytestmark = pytest.mark.gpu
@@ -76,6 +77,8 @@ def test_host_error_kinds_match_oracle(backend, args):
         backend.masked_attention(*arrs, *args[4:])
     assert e_gpu.value.kind == e_ref.value.kind
     assert str(e_gpu.value) == str(e_ref.value)
+    # the variant rebuilt from bnr_last_error_parts prints the oracle's text
+    assert error_from_parts() == (e_ref.value.kind, str(e_ref.value))
 
 
 def test_host_rope_embed_bit_exact(backend):
@@ -97,12 +100,18 @@ def test_host_rope_embed_errors(backend):
     case("host rope_embed errors")
     import bitnetrs_amd
 
-    with pytest.raises(bitnetrs_amd.InvalidConfig):
-        backend.rope_embed(np.zeros(7, f32), np.zeros(7, f32), 0, 7, 1, 1, 1e4)
-    with pytest.raises(bitnetrs_amd.InvalidConfig):
-        backend.rope_embed(np.zeros(8, f32), np.zeros(8, f32), 0, 8, 1, 1, 0.0)
-    with pytest.raises(bitnetrs_amd.InvalidShape):
-        backend.rope_embed(np.zeros(7, f32), np.zeros(8, f32), 0, 8, 1, 1, 1e4)
+    ref = oracle.CpuBackend()
+    for n_q, n_k, hd, theta, cls in [(7, 7, 7, 1e4, bitnetrs_amd.InvalidConfig),
+                                     (8, 8, 8, 0.0, bitnetrs_amd.InvalidConfig),
+                                     (0, 0, 0, 1e4, bitnetrs_amd.InvalidConfig),
+                                     (7, 8, 8, 1e4, bitnetrs_amd.InvalidShape),
+                                     (8, 7, 8, 1e4, bitnetrs_amd.InvalidShape)]:
+        with pytest.raises(cls) as e_gpu:
+            backend.rope_embed(np.zeros(n_q, f32), np.zeros(n_k, f32), 0, hd, 1, 1, theta)
+        got = error_from_parts()
+        with pytest.raises(oracle.OracleError) as e_ref:
+            ref.rope_embed(np.zeros(n_q, f32), np.zeros(n_k, f32), 0, hd, 1, 1, theta)
+        assert got == (e_ref.value.kind, str(e_ref.value)) == (e_gpu.value.kind, str(e_gpu.value))
 
 
 def test_host_decode_sequence_c1(backend):
