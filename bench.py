@@ -67,7 +67,8 @@ def per_launch_ms(torch, launch, n: int) -> float:
     return sum(ds) / len(ds)
 
 
-def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: bool = False):
+def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: bool = False,
+                 reps: int = 100):
     L, pos, cap = 4096, 4095, 4096
     g = torch.Generator(device="cuda").manual_seed(0xB17E7020)
     kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
@@ -86,7 +87,9 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: 
     torch.cuda.synchronize()
 
     # Timed region: K steps captured in one HIP graph (removes host launch
-    # overhead; the GPU still runs K separate kernels).
+    # overhead; the GPU still runs K separate kernels), replayed `reps` times;
+    # each replay is bracketed by device synchronisations and the median
+    # replay gives the per-step time.
     graph = None
     try:
         if eager:
@@ -97,78 +100,91 @@ def bench_decode(torch, be, steps: int, warmup: int, n_layers: int = 32, eager: 
             for i in range(3):
                 step(i)
         torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for i in range(steps):
-                step(i)
+        graph = capture(torch, step, steps)
         graph.replay()
         torch.cuda.synchronize()
     except Exception as e:  # capture unsupported: time eager launches
         log(f"graph capture failed ({e}); timing eager launches")
         graph = None
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
     if graph is not None:
-        graph.replay()
+        st = replay_stats(torch, graph, steps, reps=reps)
     else:
-        for i in range(steps):
-            step(i)
-    t1.record()
-    torch.cuda.synchronize()
-    ms_total = t0.elapsed_time(t1)
-    ms_step = ms_total / steps
-    # One decode_kernel launch per step: inside the graph the per-step time is
-    # the kernel's duration plus the dispatch gap between graph nodes.  The
-    # event-pair figure (spin-held queue) is reported beside it.
-    kernel_ms = ms_step if graph is not None else per_launch_ms(torch, step, min(steps, 200))
+        per = []
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0.record()
+            for i in range(steps):
+                step(i)
+            t1.record()
+            torch.cuda.synchronize()
+            per.append(t0.elapsed_time(t1) / steps)
+        per.sort()
+        st = {"median": per[len(per) // 2], "min": per[0], "p90": per[(9 * len(per)) // 10],
+              "replays": reps}
+    ms_step = st["median"]
+    # Event pairs around eager launches (spin-held queue), beside the graph.
     pair_ms = per_launch_ms(torch, step, min(steps, 200))
-    floor_ms = stream_floor_ms(torch, be, kc, vc, steps)
+    floor = stream_floor(torch, be, kc, vc, steps)
     nbytes = decode_bytes(L)
     res = {
         "ms_per_step": ms_step,
+        "stats": st,
         "gbs": nbytes / (ms_step * 1e-3) / 1e9,
-        "kernel_ms": kernel_ms,
         "pair_ms": pair_ms,
-        "kernel_gbs": nbytes / (kernel_ms * 1e-3) / 1e9,
         "bytes_per_step": nbytes,
-        "floor_ms": floor_ms,
+        "floor": floor,
         "graph": graph is not None,
+        # layer 0's inputs and the output of its last timed step, for the
+        # parity stamp (the appended row 4095 holds the rotated k, which the
+        # reference's store_kv writes there too)
         "host": {"q": q[0].cpu().numpy(), "k": k[0].cpu().numpy(), "v": v[0].cpu().numpy(),
-                 "k_cache": kc[0].cpu().numpy(), "v_cache": vc[0].cpu().numpy()},
+                 "k_cache": kc[0].cpu().numpy(), "v_cache": vc[0].cpu().numpy(),
+                 "out": out[0].cpu().numpy()},
     }
-    del kc, vc
+    del graph, kc, vc
     torch.cuda.empty_cache()
     return res
 
 
-def stream_floor_ms(torch, be, kc, vc, steps: int) -> float:
-    """A plain streaming read of the same rotated K and V caches (one layer's
-    21 MB per launch, the layers round-robin as in the decode timing), timed
-    the same way: what one launch of that many bytes can reach on this part."""
+# Shapes of the streaming floor: (threads per workgroup, 16-byte loads in
+# flight per lane, non-temporal).  (512, 1, False) is the plain one-load
+# kernel (bnr_dev_stream_read's shape).
+STREAM_SHAPES = [(512, 1, False), (256, 4, False), (256, 8, False), (256, 16, False),
+                 (512, 4, False), (512, 8, False), (1024, 2, False), (1024, 4, False),
+                 (256, 8, True), (512, 4, True), (1024, 4, True)]
+
+
+def stream_floor(torch, be, kc, vc, steps: int, nbytes: int | None = None, reps: int = 50) -> dict:
+    """Streaming reads of the same rotated K and V caches (one layer's K and
+    V per launch, the layers round-robin as in the decode timing; or, with
+    nbytes, the first nbytes/2 of all the K and of all the V caches), timed
+    the same way as the decode (median of `reps` graph replays), in every
+    shape of STREAM_SHAPES: the fastest is what one launch of that many
+    bytes can reach on this part."""
     n_layers = kc.shape[0]
-
-    def read(i):
-        r = i % n_layers
-        be.dev_stream_read(kc[r], vc[r])
-
-    for i in range(20):
-        read(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
+    if nbytes is not None:
+        half = nbytes // 2 // 16 * 4  # floats, whole 16-byte words
+        ka, va = kc.reshape(-1)[:half], vc.reshape(-1)[:half]
+    res = {}
+    for threads, loads, nt in STREAM_SHAPES:
+        if nbytes is None:
+            def read(i):
+                r = i % n_layers
+                be.dev_stream_read_shape(kc[r], vc[r], threads, loads, nt)
+        else:
+            def read(i):
+                be.dev_stream_read_shape(ka, va, threads, loads, nt)
+        for i in range(8):
             read(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1) / steps
+        torch.cuda.synchronize()
+        graph = capture(torch, read, steps)
+        res[f"{threads}x{loads}{'nt' if nt else ''}"] = replay_stats(torch, graph, steps, reps=reps)["median"]
+        del graph
+    best = min(res, key=res.get)
+    return {"ms": res[best], "shape": best, "plain_ms": res["512x1"],
+            "shapes_us": {k: round(v * 1e3, 3) for k, v in res.items()}}
 
 
 def bench_trait_path(be, steps: int = 300, pos_end: int = 4095):
@@ -260,22 +276,20 @@ def trait_timer(steps: int = 300, pos_end: int = 4095):
     return json.loads(res.stdout.strip().splitlines()[-1])
 
 
-def graph_ms(torch, launch, steps: int, reps: int = 3, restore=None, warm: int = 3) -> float:
-    """Per-launch time of `steps` launches captured in one HIP graph: the
-    fastest of `reps` replays, each after `restore()` (untimed) when given,
-    after `warm` untimed replays (a short graph's first replays after the
-    host-side setup run below the part's steady clock)."""
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            launch(i)
+def replay_stats(torch, graph, steps: int, reps: int = 100, restore=None, warm: int = 3) -> dict:
+    """Per-launch time of a HIP graph of `steps` launches: `warm` untimed
+    replays (a short graph's first replays after the host-side setup run
+    below the part's steady clock), then `reps` timed replays, each
+    bracketed by device synchronisations and preceded by `restore()`
+    (untimed) when given.  Returns the median, minimum and 90th percentile
+    over the replays of (replay time / steps), in ms."""
     for _ in range(warm):
         if restore is not None:
             restore()
         graph.replay()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    best = None
+    per = []
     for _ in range(reps):
         if restore is not None:
             restore()
@@ -284,10 +298,29 @@ def graph_ms(torch, launch, steps: int, reps: int = 3, restore=None, warm: int =
         graph.replay()
         t1.record()
         torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
-        best = ms if best is None else min(best, ms)
+        per.append(t0.elapsed_time(t1) / steps)
+    per.sort()
+    return {"median": per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1]
+                                                                       + per[len(per) // 2]),
+            "min": per[0], "p90": per[min(len(per) - 1, (9 * len(per)) // 10)], "replays": reps}
+
+
+def capture(torch, launch, steps: int):
+    """`steps` launches captured in one HIP graph."""
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch(i)
+    return graph
+
+
+def graph_ms(torch, launch, steps: int, reps: int = 50, restore=None, warm: int = 3) -> float:
+    """Median per-launch time of `steps` launches captured in one HIP graph
+    over `reps` timed replays (replay_stats)."""
+    graph = capture(torch, launch, steps)
+    st = replay_stats(torch, graph, steps, reps=reps, restore=restore, warm=warm)
     del graph
-    return best
+    return st["median"]
 
 
 def bench_decode_contexts(torch, be, contexts, steps: int = 200):
@@ -392,13 +425,18 @@ def bench_prefill(torch, be, steps: int, warmup: int, n: int = 2048):
 
     attn_ms = graph_ms(torch, attn_only, steps)
     pair_ms = per_launch_ms(torch, attn_only, max(steps, 3))
+    torch.cuda.synchronize()
     flops = prefill_flops(n)
+    # layer 0's raw inputs and the output of its last timed launch (parity)
+    host = {"q": q0[0].cpu().numpy(), "k": k0[0].cpu().numpy(), "v": v[0].cpu().numpy(),
+            "out": out[0].cpu().numpy()}
     return {"ms_per_step": ms_step, "tflops": flops / (ms_step * 1e-3) / 1e12,
             "attn_ms": attn_ms, "attn_tflops": flops / (attn_ms * 1e-3) / 1e12,
-            "pair_ms": pair_ms, "flops": flops}
+            "pair_ms": pair_ms, "flops": flops, "host": host}
 
 
-def bench_stack(torch, be, n_layers: int = 30, n_pre: int = 1024, n_dec: int = 256):
+def bench_stack(torch, be, n_layers: int = 30, n_pre: int = 1024, n_dec: int = 256,
+                dec_reps: int = 20):
     """The 30-layer stack at the 2B shape: 1024-token causal prefill of every
     layer, then 256 decode steps (every layer each step), seeded N(0,1)
     projections per layer and step.  The prefill is timed as one HIP graph
@@ -440,22 +478,23 @@ def bench_stack(torch, be, n_layers: int = 30, n_pre: int = 1024, n_dec: int = 2
             st.decode(qd[s], kd[s], vd[s], out_d[s])
     graph.replay()  # first replay writes the cache rows; replays are idempotent
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    dec_ms = t0.elapsed_time(t1)
+    dec_ms = replay_stats(torch, graph, 1, reps=dec_reps, warm=1)["median"]
     dec_bytes = n_layers * sum(decode_bytes(n_pre + s + 1) for s in range(n_dec))
     pre_flops = n_layers * prefill_flops(n_pre)
+    # layer 0's raw inputs (prefill then decode tokens) and the outputs of
+    # its last timed launches (parity)
+    host = {"q": torch.cat([q_in[0], qd[:, 0]]).cpu().numpy(),
+            "k": torch.cat([k_in[0], kd[:, 0]]).cpu().numpy(),
+            "v": torch.cat([vp[0], vd[:, 0]]).cpu().numpy(),
+            "out": torch.cat([out_p[0], out_d[:, 0]]).cpu().numpy()}
     return {"prefill_ms": pre_ms, "prefill_tflops": pre_flops / (pre_ms * 1e-3) / 1e12,
             "decode_ms": dec_ms, "decode_gbs": dec_bytes / (dec_ms * 1e-3) / 1e9,
             "decode_tok_s": n_dec / (dec_ms * 1e-3), "decode_bytes": dec_bytes,
-            "prefill_flops": pre_flops, "launches": n_layers * n_dec}
+            "prefill_flops": pre_flops, "launches": n_layers * n_dec, "host": host,
+            "decode_replays": dec_reps}
 
 
-def bench_batched(torch, be, steps: int = 50, n_seq: int = 32, cap: int = 4096):
+def bench_batched(torch, be, steps: int = 50, n_seq: int = 32, cap: int = 4096, reps: int = 50):
     """32 independent sequences, cached lengths ~ U[128, 4096) (seeded), one
     fused decode step each per launch (ragged split-K)."""
     import numpy as np
@@ -475,23 +514,23 @@ def bench_batched(torch, be, steps: int = 50, n_seq: int = 32, cap: int = 4096):
     for i in range(5):
         step(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            step(i)
+    graph = capture(torch, step, steps)
     graph.replay()
     torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    graph.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    ms = replay_stats(torch, graph, steps, reps=reps)["median"]
+    del graph
     nbytes = int(sum(decode_bytes(int(L) + 1) for L in lens))
+    floor = stream_floor(torch, be, kc, vc, steps, nbytes=nbytes)
+    # inputs and the outputs of the last timed launch, for the parity stamp:
+    # each sequence's rows 0..len-1 (row len is the appended one)
+    host = {"lens": lens, "q": q.cpu().numpy(), "k": k.cpu().numpy(), "v": v.cpu().numpy(),
+            "k_cache": [kc[b, :, :int(L)].cpu().numpy() for b, L in enumerate(lens)],
+            "v_cache": [vc[b, :, :int(L)].cpu().numpy() for b, L in enumerate(lens)],
+            "out": out.cpu().numpy()}
     del kc, vc
     torch.cuda.empty_cache()
     return {"ms_per_step": ms, "gbs": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
+            "floor": floor, "host": host,
             "lengths_min_max_mean": [int(lens.min()), int(lens.max()), float(lens.mean())]}
 
 
@@ -749,6 +788,51 @@ def load_traffic():
         return json.load(f)
 
 
+def parity(got, ref) -> dict:
+    """Error of timed outputs against the oracle on the same inputs:
+    max-abs and max-rel separately, and whether every element is within
+    |gpu - ref| <= 2e-3 + 1e-3 |ref|."""
+    import numpy as np
+
+    got = np.asarray(got, np.float64).reshape(-1)
+    ref = np.asarray(ref, np.float64).reshape(-1)
+    err = np.abs(got - ref)
+    rel = err / np.maximum(np.abs(ref), 1e-30)
+    ok = bool(np.all(np.isfinite(got)) and np.all(err <= 2e-3 + 1e-3 * np.abs(ref)))
+    return {"max_abs": float(err.max()), "max_rel": float(rel.max()), "within_tol": ok,
+            "elements": int(ref.size)}
+
+
+def oracle_decode_out(host, pos: int = 4095):
+    """The reference's rope_embed -> store_kv -> masked_attention for one token
+    of one layer (bitnet-model/src/lib.rs:1004-1036), on the oracle."""
+    import numpy as np
+
+    import oracle
+
+    be = oracle.CpuBackend()
+    q, k = host["q"].copy(), host["k"].copy()
+    be.rope_embed(q, k, pos, D, HQ, HKV, THETA)
+    kc, vc = host["k_cache"].copy(), host["v_cache"].copy()
+    kc[:, pos] = k.reshape(HKV, D)
+    vc[:, pos] = host["v"].reshape(HKV, D)
+    out = np.zeros(HQ * D, np.float32)
+    be.masked_attention(q, kc.reshape(-1), vc.reshape(-1), out, HQ, HKV, D, pos)
+    return out
+
+
+def oracle_tokens_out(q, k, v, start_pos: int = 0, cap: int | None = None):
+    """n serial per-token calls of one layer from start_pos (the reference's
+    prefill loop, bitnet-model/src/lib.rs:684-718) on the oracle; returns
+    the outputs [n, HQ*D]."""
+    import oracle
+
+    n = q.shape[0]
+    cache = oracle.KVCache(1, HKV, D, cap or start_pos + n)
+    return oracle.layer_tokens(oracle.CpuBackend(), cache, 0, q.copy(), k.copy(), v.copy(),
+                               start_pos, HQ, HKV, D, THETA)
+
+
 def cpu_baseline_decode(host, budget_s: float):
     """Reference call sequence for one decode token of one layer at pos 4095."""
     import numpy as np
@@ -802,6 +886,119 @@ def cpu_baseline_prefill(budget_s: float, n: int = 2048):
                       f"(rope_embed, store_kv, masked_attention) calls, {per:.3f} s each"}
 
 
+TIMELINE_PHASES = ["issue", "read", "barrier", "combine", "sums", "ticket", "merge"]
+
+
+def decode_timeline_main(args) -> int:
+    """Per-phase timeline of the fused decode step at 4096 rows (the headline
+    workload, 32 rotated layer caches, a HIP graph of --steps launches
+    replayed --replays times).  Loads the measurement build
+    libbitnet_hip_timeline.so, whose decode kernel stores eight 100 MHz
+    s_memrealtime stamps per workgroup: entry, loads issued, rows consumed,
+    path barrier passed, combine done (sums sent), sums complete, ticket
+    returned, merge done (merging workgroup).  Prints one JSON line of
+    medians over launches (us): the phases of the workgroup that finishes
+    last (the critical path), the same phases over all workgroups, the
+    dispatch spread, and the gap from one launch's last stamp to the next
+    launch's first."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from bitnetrs_amd import _lib
+
+    path = os.path.join(ROOT, "bitnetrs_amd", "libbitnet_hip_timeline.so")
+    if not os.path.exists(path):
+        log("libbitnet_hip_timeline.so is not built (make -C bitnetrs_amd/csrc)")
+        return 1
+    _lib.LIB_PATH = path
+    import bitnetrs_amd
+
+    lib = _lib.load()
+    lib.bnr_debug_decode_timeline.restype = ctypes.c_int
+    lib.bnr_debug_decode_timeline.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    be = bitnetrs_amd.HipBackend(0)
+    log(f"device: {be.device_name()} (timeline build)")
+    n_layers, L, pos, cap = 32, 4096, 4095, 4096
+    steps, reps = args.steps, args.replays
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7020)
+    kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+    vc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+    q = torch.randn(n_layers, HQ * D, device="cuda", generator=g) * 4.0
+    k = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+    v = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+    out = torch.zeros(n_layers, HQ * D, device="cuda")
+    max_wg = 256 * HKV  # at most 256 splits per kv head
+    stamps = torch.zeros(steps, max_wg * 8, dtype=torch.int64, device="cuda")
+
+    def step(i, rec=True):
+        r = i % n_layers
+        _lib.check(lib.bnr_debug_decode_timeline(be._h, stamps[i].data_ptr() if rec else None))
+        be.dev_decode_step(q[r], k[r], v[r], pos, HQ, HKV, D, THETA, kc[r], vc[r], cap, out[r])
+
+    for i in range(args.warmup):
+        step(i, rec=False)
+    torch.cuda.synchronize()
+    graph = capture(torch, step, steps)
+    _lib.check(lib.bnr_debug_decode_timeline(be._h, None))
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    per_step, samples, gaps, ticks_per_us = [], [], [], []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1)
+        per_step.append(ms / steps)
+        st = stamps.cpu().numpy().reshape(steps, max_wg, 8)
+        firsts, lasts = [], []
+        for i in range(steps):
+            rows = st[i][st[i][:, 0] != 0]
+            t_first = rows[:, 0].min()
+            end = rows[:, 1:].max()
+            firsts.append(t_first)
+            lasts.append(end)
+            crit = rows[np.argmax(rows[:, 7])]
+            d = np.diff(rows[:, :7], axis=1)  # issue .. ticket, every workgroup
+            merger = rows[rows[:, 7] != 0]
+            samples.append({
+                "span": end - t_first,
+                "dispatch_spread": rows[:, 0].max() - t_first,
+                "last_rows": rows[:, 2].max() - t_first,
+                "last_sums": rows[:, 5].max() - t_first,
+                "crit_start": crit[0] - t_first,
+                **{f"crit_{p}": crit[j + 1] - crit[j] for j, p in enumerate(TIMELINE_PHASES)},
+                **{f"all_{p}": np.median(d[:, j]) for j, p in enumerate(TIMELINE_PHASES[:6])},
+                **{f"all90_{p}": np.percentile(d[:, j], 90) for j, p in enumerate(TIMELINE_PHASES[:6])},
+                "all_merge": np.median(merger[:, 7] - merger[:, 6]),
+                "wgs": len(rows)})
+        gaps += [firsts[i + 1] - lasts[i] for i in range(steps - 1)]
+        ticks_per_us.append((lasts[-1] - firsts[0]) / (ms * 1e3))
+    # s_memrealtime counts at 100 MHz; the ratio of the stamps' extent to the
+    # event-timed replay checks it (a little below 100: the replay also holds
+    # the first launch's dispatch and the last one's end)
+    tick_us = 1.0 / 100.0
+    med = lambda xs: float(np.median(xs))  # noqa: E731
+    res = {"workload": "gqa_decode_step_L4096_hq20_hkv5_d128_fp32 (timeline build)",
+           "launches": len(samples), "steps": steps, "replays": reps,
+           "wgs_per_launch": int(samples[0]["wgs"]),
+           "graph_step_us": round(med(per_step) * 1e3, 3),
+           "stamp_ticks_per_us": round(med(ticks_per_us), 2),
+           "gap_to_next_launch_us": round(med(gaps) * tick_us, 3)}
+    for key in samples[0]:
+        if key != "wgs":
+            res[key + "_us"] = round(med([x[key] for x in samples]) * tick_us, 3)
+    print(json.dumps(res), flush=True)
+    be.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -828,12 +1025,22 @@ def main() -> int:
                     help="time eager launches instead of a captured graph")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run plain copies of a known size (for --pmc scaling)")
+    ap.add_argument("--replays", type=int, default=100,
+                    help="timed replays of the decode graph (the median is reported)")
+    ap.add_argument("--decode-timeline", action="store_true",
+                    help="only the per-phase timeline of the decode kernel (loads the "
+                         "measurement build libbitnet_hip_timeline.so)")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the oracle checks of the timed outputs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: measures one GPU only (asked for --gpus {args.gpus}); the attention "
               "path runs on a single GPU and has no multi-GPU launch",
               file=sys.stderr)
         return 2
+
+    if args.decode_timeline:
+        return decode_timeline_main(args)
 
     import torch
 
@@ -844,10 +1051,12 @@ def main() -> int:
     if args.copy_calibration:
         copy_calibration(torch)
     traffic = load_traffic()
-    dec = bench_decode(torch, be, args.steps, args.warmup, eager=args.eager)
-    log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step, {dec['gbs']:.0f} GB/s; kernel "
-        f"{dec['kernel_ms'] * 1e3:.2f} us, {dec['kernel_gbs']:.0f} GB/s; event pair "
-        f"{dec['pair_ms'] * 1e3:.2f} us")
+    dec = bench_decode(torch, be, args.steps, args.warmup, eager=args.eager, reps=args.replays)
+    fl = dec["floor"]
+    log(f"decode: {dec['ms_per_step'] * 1e3:.2f} us/step (median of {dec['stats']['replays']} "
+        f"replays; min {dec['stats']['min'] * 1e3:.2f}, p90 {dec['stats']['p90'] * 1e3:.2f}), "
+        f"{dec['gbs']:.0f} GB/s; event pair {dec['pair_ms'] * 1e3:.2f} us; streaming floor "
+        f"{fl['ms'] * 1e3:.2f} us ({fl['shape']}; plain one-load {fl['plain_ms'] * 1e3:.2f} us)")
     line = {
         "metric": METRIC,
         "value": round(dec["gbs"], 2),
@@ -864,17 +1073,24 @@ def main() -> int:
         "config": {"workload": "gqa_decode_step_L4096_hq20_hkv5_d128_fp32",
                    "context": 4096, "q_heads": HQ, "kv_heads": HKV, "head_dim": D,
                    "rope_theta": THETA, "layers_rotated": 32,
-                   "timed": "hip graph of fused rope+append+split-K attention launches"},
-        "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 2),
+                   "timed": f"hip graph of {args.steps} fused rope+append+split-K attention "
+                            f"launches; ms_per_step = median over {dec['stats']['replays']} "
+                            "timed replays, each bracketed by device synchronisations"},
+        "roofline": {"bound": "hbm", "achieved": round(dec["gbs"], 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("decode_reg_kernel", {}).get("bytes_per_launch"),
-                     "kernel": "decode_reg_kernel", "kernel_us": round(dec["kernel_ms"] * 1e3, 3),
+                     "kernel": "decode_reg_kernel",
+                     "graph_step_us": round(dec["ms_per_step"] * 1e3, 3),
+                     "graph_step_us_min": round(dec["stats"]["min"] * 1e3, 3),
+                     "graph_step_us_p90": round(dec["stats"]["p90"] * 1e3, 3),
                      "event_pair_us": round(dec["pair_ms"] * 1e3, 3),
                      "bytes_per_launch": dec["bytes_per_step"],
-                     "stream_floor_us": round(dec["floor_ms"] * 1e3, 3),
-                     "stream_floor_gbs": round(dec["bytes_per_step"] / (dec["floor_ms"] * 1e-3) / 1e9, 1),
-                     "frac_of_stream_floor": round(dec["floor_ms"] / dec["kernel_ms"], 4)},
+                     "stream_floor_us": round(fl["ms"] * 1e3, 3),
+                     "stream_floor_shape": fl["shape"],
+                     "stream_floor_gbs": round(dec["bytes_per_step"] / (fl["ms"] * 1e-3) / 1e9, 1),
+                     "stream_plain_us": round(fl["plain_ms"] * 1e3, 3),
+                     "frac_of_stream_floor": round(fl["ms"] / dec["ms_per_step"], 4)},
     }
     if args.decode_contexts:
         line["decode_contexts"] = bench_decode_contexts(
@@ -925,20 +1141,26 @@ def main() -> int:
                          "peak": FP32_MATRIX_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(pre["attn_tflops"] / FP32_MATRIX_PEAK_TFLOPS, 4),
                          "traffic": traffic.get("prefill_kernel", {}).get("bytes_per_launch"),
-                         "kernel": "prefill_kernel", "kernel_us": round(pre["attn_ms"] * 1e3, 3),
+                         "kernel": "prefill_kernel",
+                         "graph_launch_us": round(pre["attn_ms"] * 1e3, 3),
                          "event_pair_us": round(pre["pair_ms"] * 1e3, 3),
                          "flops_per_launch": pre["flops"]},
-            "timed": "HIP graph of one launch per layer over rotated layers (q/k restored "
-                     "between replays, untimed)"}
+            "timed": "HIP graph of one launch per layer over rotated layers, median of 50 "
+                     "timed replays (q/k restored between replays, untimed)"}
     if not args.no_batched:
         bat = bench_batched(torch, be)
         log(f"batched decode (32 seqs, ragged): {bat['ms_per_step'] * 1e3:.2f} us/step, "
-            f"{bat['gbs']:.0f} GB/s")
+            f"{bat['gbs']:.0f} GB/s; streaming floor of as many bytes "
+            f"{bat['floor']['ms'] * 1e3:.2f} us ({bat['floor']['shape']})")
         line["batched"] = {
             "workload": "gqa_decode_step_batch32_ragged_len_U128_4096_hq20_hkv5_d128_fp32",
             "value": round(bat["gbs"], 2), "unit": "GB/s", "ms_per_step": bat["ms_per_step"],
             "bytes_per_step": bat["bytes"], "frac_hbm": round(bat["gbs"] / HBM_PEAK_GBS, 4),
-            "lengths_min_max_mean": bat["lengths_min_max_mean"]}
+            "stream_floor_us": round(bat["floor"]["ms"] * 1e3, 3),
+            "stream_floor_shape": bat["floor"]["shape"],
+            "frac_of_stream_floor": round(bat["floor"]["ms"] / bat["ms_per_step"], 4),
+            "lengths_min_max_mean": bat["lengths_min_max_mean"],
+            "timed": "HIP graph of 50 batched launches, median of 50 timed replays"}
     if not args.no_stack:
         stk = bench_stack(torch, be)
         log(f"stack: prefill 30x1024 {stk['prefill_ms']:.2f} ms ({stk['prefill_tflops']:.1f} TFLOP/s); "
@@ -950,8 +1172,9 @@ def main() -> int:
             "decode_ms": round(stk["decode_ms"], 3), "decode_gbs": round(stk["decode_gbs"], 1),
             "decode_tok_s": round(stk["decode_tok_s"], 1), "decode_bytes": stk["decode_bytes"],
             "prefill_flops": stk["prefill_flops"],
-            "note": "decode timed as one HIP graph of 7680 fused decode launches; caches total "
-                    "197 MB, which fits the 256 MB MALL"}
+            "note": "prefill: one HIP graph of 60 launches, median of 50 replays; decode: one "
+                    f"HIP graph of 7680 fused decode launches, median of {stk['decode_replays']} "
+                    "replays; caches total 197 MB, which fits the 256 MB MALL"}
     if not args.no_gemv:
         gm = bench_gemv(torch, be)
         log(f"ternary gemv: token (30 layers x 7 projections, 4 launches per layer) "
@@ -994,6 +1217,36 @@ def main() -> int:
             "ms_per_token_glue_launches": round(mg["ms"], 4),
             "timed": "one HIP graph per token: 30 x 5 launches (glue in the projections' "
                      "prologues) + residual, final norm, LM head"}
+    if not args.no_parity:
+        # The timed launches' outputs against the oracle on the same inputs
+        # (outside every timed region).
+        line["parity"] = parity(dec["host"]["out"], oracle_decode_out(dec["host"]))
+        log(f"parity decode: {line['parity']}")
+        if not args.no_prefill:
+            h = pre["host"]
+            line["prefill"]["parity"] = parity(
+                h["out"], oracle_tokens_out(h["q"], h["k"], h["v"]).reshape(h["out"].shape))
+            log(f"parity prefill: {line['prefill']['parity']}")
+        if not args.no_batched:
+            import numpy as np
+
+            h = bat["host"]
+            ref = []
+            for b, L in enumerate(h["lens"]):
+                L = int(L)
+                kc = np.zeros((HKV, L + 1, D), np.float32)
+                vc = np.zeros_like(kc)
+                kc[:, :L], vc[:, :L] = h["k_cache"][b], h["v_cache"][b]
+                ref.append(oracle_decode_out({"q": h["q"][b], "k": h["k"][b], "v": h["v"][b],
+                                              "k_cache": kc, "v_cache": vc}, pos=L))
+            line["batched"]["parity"] = parity(h["out"], np.stack(ref))
+            log(f"parity batched: {line['batched']['parity']}")
+        if not args.no_stack:
+            h = stk["host"]
+            ref = oracle_tokens_out(h["q"], h["k"], h["v"])
+            line["stack"]["parity_layer0"] = parity(h["out"], ref.reshape(h["out"].shape))
+            log(f"parity stack layer 0 (1024 prefill + 256 decode outputs): "
+                f"{line['stack']['parity_layer0']}")
     if not args.no_cpu:
         log("cpu baseline (oracle) ...")
         line["cpu_baseline"] = cpu_baseline_decode(dec["host"], args.cpu_budget)

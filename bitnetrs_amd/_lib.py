@@ -119,6 +119,8 @@ SIGNATURES = {
     "bnr_dev_decode_attention": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz, _sz,
                                             _vp]),
     "bnr_dev_stream_read": (_c.c_int, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "bnr_dev_stream_read_shape": (_c.c_int, [_vp, _vp, _sz, _vp, _sz, _c.c_int, _c.c_int,
+                                             _c.c_int, _vp]),
     "bnr_dev_decode_attention_noalloc": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, _sz,
                                                     _sz, _vp]),
     "bnr_dev_decode_step": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _c.c_float, _vp,

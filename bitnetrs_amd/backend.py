@@ -170,6 +170,14 @@ class HipBackend:
         _lib.check(self._L.bnr_dev_stream_read(self._h, _dev(a, "a"), a.numel() * 4, _dev(b, "b"),
                                                b.numel() * 4, _stream(stream)))
 
+    def dev_stream_read_shape(self, a, b, threads: int, loads_per_lane: int,
+                              nontemporal: bool = False, stream=None) -> None:
+        """The streaming read in a chosen shape: workgroups of `threads`, each
+        lane with `loads_per_lane` 16-byte loads in flight (measurement)."""
+        _lib.check(self._L.bnr_dev_stream_read_shape(
+            self._h, _dev(a, "a"), a.numel() * 4, _dev(b, "b"), b.numel() * 4, threads,
+            loads_per_lane, int(nontemporal), _stream(stream)))
+
     def dev_decode_attention_noalloc(self, q, k_cache, v_cache, cap, out, n_heads, n_kv_heads,
                                      head_dim, cur_pos, stream=None) -> None:
         """dev_decode_attention without any device allocation (the merge state

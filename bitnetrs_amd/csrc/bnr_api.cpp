@@ -259,6 +259,10 @@ struct bnr_ctx {
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
   int ref_waves = 0;    // reference merge, small launches: 4 or 8 waves, 0: by length
 
+  // measurement builds (BNR_DECODE_TIMELINE): where decode launches store
+  // their phase stamps (bnr_debug_decode_timeline), or null
+  unsigned long long *timeline = nullptr;
+
   // device scratch of bnr_dev_decode_attention_noalloc (this GPU's copy)
   void *noalloc = nullptr;
   std::string noalloc_err;
@@ -913,6 +917,7 @@ int run_decode(bnr_ctx *c, DecodeArgs &a, const int *positions, int batch, int n
     if (st) return st;
     a.acc = w.acc;
   }
+  a.timeline = c->timeline;
   HIP_TRY(launch_decode(a, s), "decode launch");
   return BNR_OK;
 }
@@ -1529,6 +1534,37 @@ extern "C" int bnr_dev_stream_read(bnr_ctx *c, const void *a, size_t a_bytes, co
     return err_shape("16-byte aligned ranges of whole 16-byte words", "an unaligned range");
   DeviceGuard dg(c->device);
   HIP_TRY(launch_stream_read(a, (long long)a_bytes, b, (long long)b_bytes, (hipStream_t)stream),
+          "stream read launch");
+  return set_ok();
+}
+
+#if defined(BNR_DECODE_TIMELINE)
+// Measurement builds only (not in the public header): the next decode
+// launches of this context store kTimelineStamps stamps per workgroup at
+// `stamps` (device memory, 8 bytes each, one slot per workgroup of the grid;
+// null: none).
+extern "C" int bnr_debug_decode_timeline(bnr_ctx *c, void *stamps) {
+  if (!c) return err_backend("context is NULL");
+  c->timeline = static_cast<unsigned long long *>(stamps);
+  return set_ok();
+}
+#endif
+
+extern "C" int bnr_dev_stream_read_shape(bnr_ctx *c, const void *a, size_t a_bytes, const void *b,
+                                         size_t b_bytes, int threads, int loads_per_lane,
+                                         int nontemporal, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  if ((a_bytes && !a) || (b_bytes && !b)) return err_backend("stream_read: NULL pointer");
+  if (a_bytes % 16 || b_bytes % 16 || !aligned16(a) || !aligned16(b))
+    return err_shape("16-byte aligned ranges of whole 16-byte words", "an unaligned range");
+  if (threads < 64 || threads > 1024 || threads % 64)
+    return err_config(fmt("threads must be a multiple of 64 in 64..=1024, got %d", threads));
+  if (loads_per_lane != 1 && loads_per_lane != 2 && loads_per_lane != 4 && loads_per_lane != 8 &&
+      loads_per_lane != 16)
+    return err_config(fmt("loads_per_lane must be 1, 2, 4, 8 or 16, got %d", loads_per_lane));
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_stream_read_shape(a, (long long)a_bytes, b, (long long)b_bytes, threads,
+                                   loads_per_lane, nontemporal != 0, (hipStream_t)stream),
           "stream read launch");
   return set_ok();
 }

@@ -119,8 +119,35 @@ __device__ __forceinline__ void ref_merge(const DecodeArgs &a, int b, int h, flo
 // last bits of an output can differ between runs (the two older merges of
 // decode_kernel are deterministic).
 // ---------------------------------------------------------------------------
+// Phase stamps of a measurement build (BNR_DECODE_TIMELINE): wave 0 reads
+// the 100 MHz real-time counter at the ends of the phases and thread 0
+// stores them when the workgroup ends.  Scheduling barriers keep each read
+// between the instructions of the phases it separates.
+#if defined(BNR_DECODE_TIMELINE)
+#define BNR_STAMP(k)                                   \
+  do {                                                 \
+    __builtin_amdgcn_sched_barrier(0);                 \
+    stamp[k] = __builtin_amdgcn_s_memrealtime();       \
+    __builtin_amdgcn_sched_barrier(0);                 \
+  } while (0)
+#else
+#define BNR_STAMP(k) ((void)0)
+#endif
+
 template <int G, int W, int RPG, bool RAGGED>
 __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
+#if defined(BNR_DECODE_TIMELINE)
+  unsigned long long stamp[kTimelineStamps] = {};
+  stamp[0] = __builtin_amdgcn_s_memrealtime();
+  auto flush_stamps = [&]() {
+    if (threadIdx.x == 0 && a.timeline) {
+      const long long wg = blockIdx.x + (long long)gridDim.x * (blockIdx.y + (long long)gridDim.y * blockIdx.z);
+      for (int k = 0; k < kTimelineStamps; ++k) a.timeline[wg * kTimelineStamps + k] = stamp[k];
+    }
+  };
+#else
+  auto flush_stamps = []() {};
+#endif
   constexpr int D = kHeadDim;
   constexpr int NRG = 4 * W;  // row groups
   static_assert(G * D <= kAccL && G <= 4, "accumulator layout holds up to 4 q heads");
@@ -135,7 +162,10 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   const int b = blockIdx.z;
   const int s = blockIdx.x;
   const int nsplit = a.split_off[b + 1] - a.split_off[b];
-  if (RAGGED && s >= nsplit) return;
+  if (RAGGED && s >= nsplit) {
+    flush_stamps();
+    return;
+  }
   const int h = blockIdx.y;
   const int pos = a.positions[b];
   const int L = pos + 1;
@@ -190,6 +220,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   };
   load_pass(t0);
   __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the math
+  BNR_STAMP(1);
 
   if (rope) {
 #pragma unroll
@@ -271,6 +302,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       }
     }
   }
+  BNR_STAMP(2);
   // ---- the row groups add through LDS (fast path) ----
   // Written before the barrier that decides the path (one barrier fewer):
   // the exact path discards these sums and rewrites s_o after it.
@@ -289,6 +321,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   const bool wave_over = __ballot(over) != 0;  // every lane votes
   if ((tid & 63) == 0) s_over[tid >> 6] = wave_over;
   __syncthreads();
+  BNR_STAMP(3);
   bool exact = false;
 #pragma unroll
   for (int w = 0; w < W; ++w) exact |= s_over[w] != 0;
@@ -318,6 +351,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     }
     if (nsplit == 1) {
       signal();
+      flush_stamps();
       return;
     }
     if (tid < G) {
@@ -389,6 +423,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     }
     if (nsplit == 1) {
       signal();
+      flush_stamps();
       return;
     }
     if (tid < G) {
@@ -406,7 +441,9 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   // Every wave's device-scope adds and partial stores have completed before
   // the ticket is taken; the merging workgroup reads them with atomic
   // read-modify-writes (ref_merge).
+  BNR_STAMP(4);
   __builtin_amdgcn_s_waitcnt(0);
+  BNR_STAMP(5);
   if (tid < G) s_R[tid] = R[tid];
   __syncthreads();
   // Host-slice calls: split 0's rotated q and k (in host memory) reach the
@@ -421,10 +458,19 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     s_last = (ticket == (unsigned)(nsplit - 1));
   }
   __syncthreads();
-  if (!s_last) return;
+  BNR_STAMP(6);
+  if (!s_last) {
+    flush_stamps();
+    return;
+  }
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
   signal();
+#if defined(BNR_DECODE_TIMELINE)
+  __builtin_amdgcn_s_waitcnt(0);  // the output stores have completed
+  BNR_STAMP(7);
+#endif
+  flush_stamps();
 }
 
 template <int G, int W, bool RAGGED>

@@ -90,9 +90,18 @@ struct DecodeArgs {
   // into done[b * n_kv + h] once that output is visible to the host.
   unsigned *done;
   unsigned seq;
+  // Measurement builds only (compiled with BNR_DECODE_TIMELINE): when
+  // non-null, every workgroup of the reference-merge kernel stores
+  // kTimelineStamps s_memrealtime stamps (100 MHz) at
+  // timeline[linear block index * kTimelineStamps].  Ignored otherwise.
+  unsigned long long *timeline;
   int positions[kMaxBatchPerLaunch];
   int split_off[kMaxBatchPerLaunch + 1];
 };
+// Stamps per workgroup of a timeline build: entry, loads issued, rows
+// consumed, path barrier passed, combine done (sums sent), sums complete,
+// ticket returned, merge done (merging workgroup only, else 0).
+constexpr int kTimelineStamps = 8;
 hipError_t launch_decode(const DecodeArgs &a, hipStream_t s);
 // The reference-merge kernel alone (a.merge_ref; group 1, 2 or 4).
 hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s);
@@ -156,6 +165,12 @@ hipError_t launch_decode_generic(const DecodeGenericArgs &a, hipStream_t s);
 // measurement.
 hipError_t launch_stream_read(const void *a, long long a_bytes, const void *b, long long b_bytes,
                               hipStream_t s);
+// The same read with `loads` (1, 2, 4, 8 or 16) 16-byte loads in flight per
+// lane, workgroups of `threads` (a multiple of 64, <= 1024), non-temporal
+// loads when nt.
+hipError_t launch_stream_read_shape(const void *a, long long a_bytes, const void *b,
+                                    long long b_bytes, int threads, int loads, bool nt,
+                                    hipStream_t s);
 
 // Causal flash prefill (head_dim 128, fp32 MFMA): query i of the n_tokens
 // (position start_pos + i) attends cache rows 0..start_pos+i.

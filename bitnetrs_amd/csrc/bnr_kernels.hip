@@ -663,6 +663,38 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const float4 *a, long 
   if (sum == -1.2345e-30f && i < na) const_cast<float4 *>(a)[i] = v;
 }
 
+// Streaming read of two device ranges, laid end to end, in one round over
+// the CUs: workgroup w reads float4 words [w NL T, (w+1) NL T) (T threads),
+// each lane issuing its NL 16-byte loads (words T apart) before
+// it uses any of them, so NL loads per lane are in flight at once; NT: the
+// loads are non-temporal.  The sum of a lane's words is stored only if it
+// equals an impossible value, so no load is removed.
+template <int NL, bool NT>
+__global__ __launch_bounds__(1024) void stream_read_nl_kernel(const float4 *a, long long na,
+                                                              const float4 *b, long long nb) {
+  const long long base = (long long)blockIdx.x * NL * blockDim.x + threadIdx.x;
+  float4 v[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const long long idx = base + (long long)i * blockDim.x;
+    const float4 *p = idx < na ? a + idx : (idx - na < nb ? b + (idx - na) : nullptr);
+    v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p) {
+      if constexpr (NT) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v w = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+        v[i] = make_float4(w.x, w.y, w.z, w.w);
+      } else {
+        v[i] = *p;
+      }
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  if (sum == -1.2345e-30f && base < na) const_cast<float4 *>(a)[base] = v[0];
+}
+
 template <int G, bool INLINE, bool RAGGED>
 hipError_t launch_decode_gir(const DecodeArgs &a, hipStream_t s) {
   dim3 grid(a.max_splits, a.n_kv, a.batch), block(256);
@@ -753,6 +785,34 @@ hipError_t launch_stream_read(const void *a, long long a_bytes, const void *b, l
   if (wgs > 0x7fffffffLL) return hipErrorInvalidValue;
   stream_read_kernel<<<dim3((unsigned)wgs), dim3(512), 0, s>>>(
       static_cast<const float4 *>(a), na, static_cast<const float4 *>(b), nb);
+  return hipGetLastError();
+}
+
+hipError_t launch_stream_read_shape(const void *a, long long a_bytes, const void *b,
+                                    long long b_bytes, int threads, int loads, bool nt,
+                                    hipStream_t s) {
+  const long long na = a_bytes / 16, nb = b_bytes / 16;
+  if (na + nb == 0) return hipSuccess;
+  if (threads < 64 || threads > 1024 || threads % 64) return hipErrorInvalidValue;
+  const long long per_wg = (long long)threads * loads;
+  const long long wgs = (na + nb + per_wg - 1) / per_wg;
+  if (wgs > 0x7fffffffLL) return hipErrorInvalidValue;
+  const float4 *pa = static_cast<const float4 *>(a), *pb = static_cast<const float4 *>(b);
+  const dim3 grid((unsigned)wgs), block((unsigned)threads);
+#define BNR_STREAM_CASE(NL)                                                          \
+  case NL:                                                                           \
+    if (nt) stream_read_nl_kernel<NL, true><<<grid, block, 0, s>>>(pa, na, pb, nb);  \
+    else stream_read_nl_kernel<NL, false><<<grid, block, 0, s>>>(pa, na, pb, nb);    \
+    break;
+  switch (loads) {
+    BNR_STREAM_CASE(1)
+    BNR_STREAM_CASE(2)
+    BNR_STREAM_CASE(4)
+    BNR_STREAM_CASE(8)
+    BNR_STREAM_CASE(16)
+    default: return hipErrorInvalidValue;
+  }
+#undef BNR_STREAM_CASE
   return hipGetLastError();
 }
 

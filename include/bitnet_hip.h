@@ -388,6 +388,14 @@ int bnr_kv_dev_prefill(bnr_ctx *ctx, bnr_kv_cache *cache, size_t layer, float *q
  * reads, as the floor a single launch of that many bytes can reach. */
 int bnr_dev_stream_read(bnr_ctx *ctx, const void *a, size_t a_bytes, const void *b,
                         size_t b_bytes, void *stream);
+/* The same read in a chosen shape, no counterpart in the reference:
+ * workgroups of `threads` (a multiple of 64 up to 1024), each lane issuing
+ * `loads_per_lane` (1, 2, 4, 8 or 16) 16-byte loads before using any, so
+ * that many are in flight per lane; non-temporal loads when nontemporal != 0.
+ * The benchmark takes the fastest shape as the streaming floor. */
+int bnr_dev_stream_read_shape(bnr_ctx *ctx, const void *a, size_t a_bytes, const void *b,
+                              size_t b_bytes, int threads, int loads_per_lane, int nontemporal,
+                              void *stream);
 
 #ifdef __cplusplus
 }
