@@ -977,6 +977,12 @@ def decode_timeline_main(args) -> int:
                 **{f"all_{p}": np.median(d[:, j]) for j, p in enumerate(TIMELINE_PHASES[:6])},
                 **{f"all90_{p}": np.percentile(d[:, j], 90) for j, p in enumerate(TIMELINE_PHASES[:6])},
                 "all_merge": np.median(merger[:, 7] - merger[:, 6]),
+                # when the workgroups pass their path barrier (all rows in), from the first entry
+                "rows_in_p10": np.percentile(rows[:, 3] - t_first, 10),
+                "rows_in_p50": np.percentile(rows[:, 3] - t_first, 50),
+                "rows_in_p90": np.percentile(rows[:, 3] - t_first, 90),
+                "rows_in_max": rows[:, 3].max() - t_first,
+                "entry_p90": np.percentile(rows[:, 0] - t_first, 90),
                 "wgs": len(rows)})
         gaps += [firsts[i + 1] - lasts[i] for i in range(steps - 1)]
         ticks_per_us.append((lasts[-1] - firsts[0]) / (ms * 1e3))
@@ -994,6 +1000,36 @@ def decode_timeline_main(args) -> int:
     for key in samples[0]:
         if key != "wgs":
             res[key + "_us"] = round(med([x[key] for x in samples]) * tick_us, 3)
+    # The phases' hardware floors: one lane's chain of dependent device-scope
+    # operations (the merge chain is made of them), and a graph of empty
+    # launches of the same grid (the launch-to-launch cost).
+    lib.bnr_debug_rt_probe.restype = ctypes.c_int
+    lib.bnr_debug_rt_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p, ctypes.c_void_p]
+    lib.bnr_debug_empty_launch.restype = ctypes.c_int
+    lib.bnr_debug_empty_launch.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    buf = torch.zeros(256, dtype=torch.int32, device="cuda")
+    out = torch.zeros(2, dtype=torch.int64, device="cuda")
+    n_ops = 2000
+    for mode, name in enumerate(["fetch_add_return", "add_then_wait", "exchange", "agent_load"]):
+        ticks = []
+        for _ in range(5):
+            _lib.check(lib.bnr_debug_rt_probe(be._h, buf.data_ptr(), n_ops, mode, out.data_ptr(), None))
+            torch.cuda.synchronize()
+            ticks.append(int(out[0].item()))
+        res[f"rt_{name}_us"] = round(med(ticks) * tick_us / n_ops, 4)
+    wgs = int(samples[0]["wgs"])
+    wbuf = torch.zeros(64 * 256, dtype=torch.int32, device="cuda")
+    for mode, name in enumerate(["bare", "args", "lds64k", "args_lds64k", "store", "nt_store",
+                                 "atomic_add", "system_store", "decode_footprint"]):
+        # on the capturing stream (a NULL stream would not be captured)
+        empty = capture(torch, lambda i: _lib.check(lib.bnr_debug_empty_launch(
+            be._h, wgs, 512, mode, wbuf.data_ptr(),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))), steps)
+        res[f"empty_launch_{name}_graph_step_us"] = round(
+            replay_stats(torch, empty, steps, reps=reps)["median"] * 1e3, 3)
+        del empty
     print(json.dumps(res), flush=True)
     be.close()
     return 0
@@ -1090,6 +1126,7 @@ def main() -> int:
                      "stream_floor_shape": fl["shape"],
                      "stream_floor_gbs": round(dec["bytes_per_step"] / (fl["ms"] * 1e-3) / 1e9, 1),
                      "stream_plain_us": round(fl["plain_ms"] * 1e3, 3),
+                     "stream_shapes_us": fl["shapes_us"],
                      "frac_of_stream_floor": round(fl["ms"] / dec["ms_per_step"], 4)},
     }
     if args.decode_contexts:

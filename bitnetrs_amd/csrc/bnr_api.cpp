@@ -1548,6 +1548,39 @@ extern "C" int bnr_debug_decode_timeline(bnr_ctx *c, void *stamps) {
   c->timeline = static_cast<unsigned long long *>(stamps);
   return set_ok();
 }
+
+namespace bnr {
+hipError_t launch_rt_probe(unsigned *buf, int n, int mode, unsigned long long *out, hipStream_t s);
+hipError_t launch_empty(int wgs, int threads, int mode, unsigned *buf, hipStream_t s);
+}  // namespace bnr
+
+// Round trips of device-scope operations (one lane, n dependent operations
+// of the given mode on buf, at least 512 bytes of zeroed device memory;
+// out[0] = elapsed 100 MHz ticks).
+extern "C" int bnr_debug_rt_probe(bnr_ctx *c, void *buf, int n, int mode, void *out, void *stream) {
+  if (!c || !buf || !out || n < 1 || mode < 0 || mode > 3) return err_backend("rt_probe: bad arguments");
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_rt_probe(static_cast<unsigned *>(buf), n, mode,
+                          static_cast<unsigned long long *>(out), (hipStream_t)stream),
+          "rt_probe launch");
+  return set_ok();
+}
+
+// An empty launch of wgs workgroups of `threads` threads (at most 512);
+// mode 0 bare, 1 with the decode's argument block, 2 with 64 KB of LDS,
+// 3 with both; 4-7: one word per workgroup written into buf (at least 64 KB
+// of device memory): a plain store, a non-temporal store, a device-scope
+// atomic add, a system-scope store; 8: the argument block, 64 KB of LDS
+// and 160 VGPRs (the 8-wave decode kernel's footprint).
+extern "C" int bnr_debug_empty_launch(bnr_ctx *c, int wgs, int threads, int mode, void *buf,
+                                      void *stream) {
+  if (!c || wgs < 1 || threads < 1 || threads > 512 || mode < 0 || mode > 8 || (mode >= 4 && mode <= 7 && !buf))
+    return err_backend("empty_launch: bad arguments");
+  DeviceGuard dg(c->device);
+  HIP_TRY(launch_empty(wgs, threads, mode, static_cast<unsigned *>(buf), (hipStream_t)stream),
+          "empty launch");
+  return set_ok();
+}
 #endif
 
 extern "C" int bnr_dev_stream_read_shape(bnr_ctx *c, const void *a, size_t a_bytes, const void *b,

@@ -208,14 +208,14 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       const int t = tp + i * NRG + rg;
       valid[i] = t < t1;
       const long long off = (long long)(valid[i] ? t : t0) * D;
-      klo[i] = ld4(kc + off + 4 * j);
-      khi[i] = ld4(kc + off + 64 + 4 * j);
+      klo[i] = ld4_nt(kc + off + 4 * j);
+      khi[i] = ld4_nt(kc + off + 64 + 4 * j);
     }
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
       const long long off = (long long)(valid[i] ? tp + i * NRG + rg : t0) * D;
-      vlo[i] = ld4(vc + off + 4 * j);
-      vhi[i] = ld4(vc + off + 64 + 4 * j);
+      vlo[i] = ld4_nt(vc + off + 4 * j);
+      vhi[i] = ld4_nt(vc + off + 64 + 4 * j);
     }
   };
   load_pass(t0);
@@ -488,7 +488,93 @@ hipError_t launch_reg_wr(const DecodeArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+#if defined(BNR_DECODE_TIMELINE)
+// Measurement builds only.  One lane runs n dependent device-scope
+// operations (each address depends on the previous result, or an
+// s_waitcnt separates them) and stores the elapsed 100 MHz ticks: the round
+// trip of the operations the decode's merge chain is made of.  mode 0:
+// fetch_add with return (the ticket); 1: add without return, then wait for
+// it (the sums); 2: exchange (the merging read); 3: agent-scope load.
+__global__ void rt_probe_kernel(unsigned *buf, int n, int mode, unsigned long long *out) {
+  if (threadIdx.x != 0) return;
+  unsigned v = 1;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < n; ++i) {
+    unsigned *p = buf + 64 * (v & 1);
+    if (mode == 0) {
+      v += __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (mode == 1) {
+      (void)__hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      v += 2;
+    } else if (mode == 2) {
+      v += __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      v += __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  out[0] = t1 - t0;
+  out[1] = v;
+}
+
+// Launches that do (almost) nothing: the graph's launch-to-launch cost of
+// a grid, bare, with the decode's argument block (one value read from it),
+// with a 64 KB LDS allocation (one word written and read), or both.
+__global__ void empty_kernel() {}
+__global__ void empty_args_kernel(DecodeArgs a) {
+  if (threadIdx.x == 0 && a.seq == 0x7fffffffu) a.counters[0] = 0;  // never true
+}
+__global__ __launch_bounds__(512) void empty_lds_kernel(unsigned flag) {
+  __shared__ float s_big[16384];
+  s_big[threadIdx.x * 32] = (float)threadIdx.x;
+  __syncthreads();
+  if (s_big[(threadIdx.x * 37) & 16383] == -1.f && flag == 0x7fffffffu) s_big[0] = 1.f;
+}
+// ... or one word per workgroup written to buf: mode 4 a plain store, 5 a
+// non-temporal store, 6 a device-scope atomic add, 7 a system-scope store.
+__global__ void empty_write_kernel(unsigned *buf, int mode) {
+  if (threadIdx.x != 0) return;
+  unsigned *p = buf + 64 * (blockIdx.x & 255);
+  if (mode == 4) *p = blockIdx.x;
+  else if (mode == 5) __builtin_nontemporal_store((unsigned)blockIdx.x, p);
+  else if (mode == 6) (void)__hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else __hip_atomic_store(p, (unsigned)blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__global__ __launch_bounds__(512) void empty_args_lds_kernel(DecodeArgs a) {
+  __shared__ float s_big[16384];
+  s_big[threadIdx.x * 32] = (float)threadIdx.x;
+  __syncthreads();
+  if (s_big[(threadIdx.x * 37) & 16383] == -1.f && a.seq == 0x7fffffffu) a.counters[0] = 0;
+}
+// ... and with 160 VGPRs allocated, as the 8-wave decode kernel has.
+__global__ __launch_bounds__(512) void empty_full_kernel(DecodeArgs a) {
+  __shared__ float s_big[16384];
+  asm volatile("v_mov_b32 v159, 0" ::: "v159");
+  s_big[threadIdx.x * 32] = (float)threadIdx.x;
+  __syncthreads();
+  if (s_big[(threadIdx.x * 37) & 16383] == -1.f && a.seq == 0x7fffffffu) a.counters[0] = 0;
+}
+#endif
+
 }  // namespace
+
+#if defined(BNR_DECODE_TIMELINE)
+hipError_t launch_rt_probe(unsigned *buf, int n, int mode, unsigned long long *out, hipStream_t s) {
+  rt_probe_kernel<<<1, 64, 0, s>>>(buf, n, mode, out);
+  return hipGetLastError();
+}
+hipError_t launch_empty(int wgs, int threads, int mode, unsigned *buf, hipStream_t s) {
+  DecodeArgs a{};
+  if (mode >= 4 && mode <= 7) empty_write_kernel<<<wgs, threads, 0, s>>>(buf, mode);
+  else if (mode == 0) empty_kernel<<<wgs, threads, 0, s>>>();
+  else if (mode == 1) empty_args_kernel<<<wgs, threads, 0, s>>>(a);
+  else if (mode == 2) empty_lds_kernel<<<wgs, threads, 0, s>>>(0u);
+  else if (mode == 3) empty_args_lds_kernel<<<wgs, threads, 0, s>>>(a);
+  else empty_full_kernel<<<wgs, threads, 0, s>>>(a);
+  return hipGetLastError();
+}
+#endif
 
 hipError_t launch_decode_ref(const DecodeArgs &a, hipStream_t s) {
   if (!a.acc) return hipErrorInvalidValue;

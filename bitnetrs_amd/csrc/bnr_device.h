@@ -101,6 +101,16 @@ __device__ __forceinline__ float4 ld4(const float *p) {
   return *reinterpret_cast<const float4 *>(p);
 }
 
+// 16 bytes with the non-temporal hint (global_load_dwordx4 ... nt), for
+// data read once: the K/V rows of a decode step.  Measured on MI355X: a
+// single-sequence step at 4096 rows 9.42 -> 8.60 us, and plain streaming
+// reads of the same 21 MB 5.42 -> 4.98 us.
+__device__ __forceinline__ float4 ld4_nt(const float *p) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void st4(float *p, float4 v) {
   *reinterpret_cast<float4 *>(p) = v;
 }

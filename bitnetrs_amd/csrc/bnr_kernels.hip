@@ -299,14 +299,14 @@ void decode_kernel(DecodeArgs a) {
       const int t = tp + i * 16 + rg;
       valid[i] = t < t1;
       const long long off = (long long)(valid[i] ? t : t0) * D;
-      klo[i] = ld4(kc + off + 4 * j);
-      khi[i] = ld4(kc + off + 64 + 4 * j);
+      klo[i] = ld4_nt(kc + off + 4 * j);
+      khi[i] = ld4_nt(kc + off + 64 + 4 * j);
     }
 #pragma unroll
     for (int i = 0; i < RPG; ++i) {
       const long long off = (long long)(valid[i] ? tp + i * 16 + rg : t0) * D;
-      vlo[i] = ld4(vc + off + 4 * j);
-      vhi[i] = ld4(vc + off + 64 + 4 * j);
+      vlo[i] = ld4_nt(vc + off + 4 * j);
+      vhi[i] = ld4_nt(vc + off + 64 + 4 * j);
     }
   };
   load_pass(t0);
