@@ -113,6 +113,7 @@ SIGNATURES = {
     "bnr_masked_attention": (_c.c_int, [_vp, _f, _sz, _f, _sz, _f, _sz, _f, _sz, _sz, _sz, _sz,
                                         _sz]),
     "bnr_set_mirror_mode": (_c.c_int, [_vp, _c.c_int]),
+    "bnr_set_deterministic": (_c.c_int, [_vp, _c.c_int]),
     "bnr_mirror_invalidate": (_c.c_int, [_vp]),
     "bnr_dev_rope_append": (_c.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _sz, _c.c_float,
                                        _vp, _vp, _sz, _vp]),

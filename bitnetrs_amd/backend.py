@@ -148,6 +148,11 @@ class HipBackend:
     def set_mirror_mode(self, mode: int) -> None:
         _lib.check(self._L.bnr_set_mirror_mode(self._h, mode))
 
+    def set_deterministic(self, on: bool = True) -> None:
+        """Decode launches merge their splits in a fixed order: the same
+        inputs give the same output bits on every run (slower)."""
+        _lib.check(self._L.bnr_set_deterministic(self._h, int(bool(on))))
+
     def mirror_invalidate(self) -> None:
         _lib.check(self._L.bnr_mirror_invalidate(self._h))
 

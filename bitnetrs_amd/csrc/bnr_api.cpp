@@ -254,7 +254,8 @@ struct bnr_ctx {
   int large_wgs = 1024;
   int force_rpg = 0;
   int min_passes = 1;
-  int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel ticket; 2: reference merge
+  int merge_mode = -1;  // -1: planner decides; 0: second kernel; 1: in-kernel ticket; 2: reference merge;
+                        // 3: reference merge, deterministic
   int split_cost = -1;  // planner cost of a split of the in-kernel merges (ns); -1: mode default
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
   int ref_waves = 0;    // reference merge, small launches: 4 or 8 waves, 0: by length
@@ -354,9 +355,24 @@ int get_host(bnr_ctx *c, void *host, const void *dev, size_t bytes, const char *
 // Grow-only zero-copy staging: pinned, non-coherent host memory mapped into
 // the device's address space.  The kernels of the per-token host-slice
 // entry points read their inputs from it and write their outputs into it,
-// so such a call issues no copy commands.  Non-coherent host memory is
-// coherent at kernel boundaries: the host fills it before the launch and
-// reads it after host_wait.
+// so such a call issues no copy commands.  What makes it safe without a
+// stream synchronisation:
+//  - outputs: a workgroup that wrote outputs into the staging makes them
+//    host-visible before its completion word does -- signal_host waits for
+//    the workgroup's stores and then stores the word with a system-scope
+//    release, which writes this XCD's L2 back.  The rotated q and k of the
+//    fused decode are written by split 0, which is not always the
+//    workgroup that stores the word: split 0 issues a system-scope release
+//    fence before its ticket, so they reach the host before the merging
+//    workgroup (which takes the last ticket) stores the word.  The host
+//    reads the staging only after every word of the call holds its
+//    sequence number (host_wait_words), even though a kernel may still be
+//    resident then;
+//  - inputs: the host rewrites the staging only for the next call, after
+//    every word of this one was set, i.e. after every workgroup of this
+//    call has read its inputs.
+// tests/test_gpu_host_words.py checks back-to-back host calls, each output
+// checked on return.
 int ensure_zc(bnr_ctx *c, size_t n) {
   if (c->h_zc_n >= n && c->h_zc) return BNR_OK;
   if (c->h_zc) {
@@ -741,7 +757,8 @@ void bnr::plan_decode(const DecodePlanConfig &cfg, const int *lens, int batch, i
   const bool large = batch > 1 && wgs4 >= c->large_wgs;
   const int mode = c->merge_mode >= 0 ? c->merge_mode : 2;
   a.merge_inline = mode != 0;
-  a.merge_ref = mode == 2;
+  a.merge_ref = mode >= 2;
+  a.merge_det = mode == 3;
   const long long split_cost = c->split_cost >= 0 ? c->split_cost : 61;
   int passes = 1;
   if (a.merge_ref) {
@@ -1017,7 +1034,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   }
   c->target_wgs = c->n_cu;
   if (const char *v = std::getenv("BNR_DECODE_TARGET_WGS")) c->target_wgs = std::max(1, atoi(v));
-  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = std::min(2, std::max(0, atoi(v)));
+  if (const char *v = std::getenv("BNR_DECODE_MERGE")) c->merge_mode = std::min(3, std::max(0, atoi(v)));
   if (const char *v = std::getenv("BNR_DECODE_SPLIT_COST")) c->split_cost = std::max(0, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_ROWS")) c->ref_rows = std::max(0, atoi(v));
   if (const char *v = std::getenv("BNR_DECODE_REF_WAVES")) c->ref_waves = atoi(v) == 8 ? 8 : 4;
@@ -1061,6 +1078,7 @@ extern "C" void bnr_destroy(bnr_ctx *c) {
     if (c->pf_counters) (void)hipFree(c->pf_counters);
     if (c->pf_queue) (void)hipFree(c->pf_queue);
     if (c->stream) (void)hipStreamDestroy(c->stream);
+    noalloc_release(c->device, c);
   }
   delete c;
 }
@@ -1264,6 +1282,13 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     m->synced = 0;
     return err_hip(e, "masked_attention");
   }
+  return set_ok();
+}
+
+extern "C" int bnr_set_deterministic(bnr_ctx *c, int on) {
+  if (!c) return err_backend("context is NULL");
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->merge_mode = on ? 3 : -1;
   return set_ok();
 }
 
@@ -1624,6 +1649,11 @@ extern "C" int bnr_dev_decode_attention_noalloc(bnr_ctx *c, const float *q, cons
     return err_shape(fmt("cur_pos < %d", INT32_MAX), fmt("cur_pos = %zu", cur_pos));
   std::lock_guard<std::mutex> lk(c->mu);
   if (!c->noalloc) return err_backend(c->noalloc_err.empty() ? "no-alloc scratch unavailable" : c->noalloc_err);
+  if (!noalloc_claim(c->device, c, stream))
+    return err_backend(fmt("decode_attention_noalloc: GPU %d's scratch is held by another context "
+                           "or stream (launches from two could overlap on the GPU and race); "
+                           "use one context and one stream, or destroy the other context first",
+                           c->device));
   DeviceGuard dg(c->device);
   DecodeArgs a{};
   a.q = q;

@@ -82,6 +82,90 @@ __device__ __forceinline__ void ref_merge(const DecodeArgs &a, int b, int h, flo
   }
 }
 
+// The deterministic form of the merge (merge_det): every split stored its
+// (m, l, O) -- m = R for a split on the reference path, its own maximum on
+// the exact path -- with agent-scope stores, and the last workgroup of
+// (sequence b, kv head h) combines them in a fixed order: the maxima and
+// weights w_s = exp2(m_s - M) in a fixed tree, then for every output the
+// splits in split order.  When every split used the reference, every w_s is
+// exp2(0) = 1 and the result is a sum in a fixed order.  The bits of the
+// output do not depend on the order in which the splits finished.  s_ml:
+// LDS for nsplit * G (m, l) pairs; s_wt: LDS for kMaxSplits * G weights,
+// then one float4 per thread.
+template <int G>
+__device__ __forceinline__ void det_merge(const DecodeArgs &a, int b, int h, int nsplit,
+                                          float2 *s_ml, float *s_wt, float *s_L, int tid,
+                                          int nthreads) {
+  constexpr int D = kHeadDim;
+  const long long s0 = a.split_off[b];
+  for (int i = tid; i < nsplit * G; i += nthreads) {  // i = s * G + g
+    const float *ml = reinterpret_cast<const float *>(&a.ws_ml[((s0 + i / G) * a.n_kv + h) * G + i % G]);
+    s_ml[i] = make_float2(ld_agent(ml), ld_agent(ml + 1));
+  }
+  __syncthreads();
+  // wave g: the maximum over the splits, then the weights and the weight sum
+  // (lane-strided partial sums, then a fixed tree over the lanes)
+  const int wave = tid >> 6, lane = tid & 63;
+  if (wave < G) {
+    const int g = wave;
+    float M = -INFINITY;
+    for (int sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, s_ml[sp * G + g].x);
+    M = wave_max(M);
+    float Lp = 0.f;
+    for (int sp = lane; sp < nsplit; sp += 64) {
+      const float2 v = s_ml[sp * G + g];
+      const float wgt = v.x > -INFINITY ? fast_exp2(v.x - M) : 0.f;
+      s_wt[sp * G + g] = wgt;
+      Lp = fmaf(wgt, v.y, Lp);
+    }
+    const float Ls = wave_sum(Lp);
+    if (lane == 0) s_L[g] = Ls;
+  }
+  __syncthreads();
+  // Thread t: the float4 of outputs 4 q4 .. 4 q4 + 3 (q4 = t % NQ), over
+  // the splits sp = sg, sg + NSG, ... in order (sg = t / NQ), with 16-byte
+  // agent-scope loads (buffer loads with sc1); then the NSG partial sums of
+  // a quad add in sg order.
+  constexpr int NQ = G * D / 4;
+  const int nsg = nthreads / NQ, q4 = tid % NQ, sg = tid / NQ, g = 4 * q4 / D;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(a.ws_o + (s0 * a.n_kv + h) * G * D), (short)0, 0x7fffffff, 0x00020000);
+  const int stride_b = a.n_kv * G * D * 4;  // bytes from one split to the next
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp0 = sg; sp0 < nsplit; sp0 += 8 * nsg) {
+    float4 x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int sp = sp0 + i * nsg;
+      typedef float f4v __attribute__((ext_vector_type(4)));
+      const f4v v = __builtin_bit_cast(
+          f4v, __builtin_amdgcn_raw_buffer_load_b128(ro, (sp < nsplit ? sp : 0) * stride_b + 16 * q4, 0, 16));
+      x[i] = make_float4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int sp = sp0 + i * nsg;
+      if (sp < nsplit) O = axpy4(s_wt[sp * G + g], x[i], O);
+    }
+  }
+  float4 *s_part = reinterpret_cast<float4 *>(s_wt + kMaxSplits * G);
+  s_part[tid] = O;
+  __syncthreads();
+  if (tid < NQ) {
+    float4 T = s_part[tid];
+    for (int k = 1; k < nsg; ++k) {
+      const float4 y = s_part[k * NQ + tid];
+      T.x += y.x;
+      T.y += y.y;
+      T.z += y.z;
+      T.w += y.w;
+    }
+    const float Ls = s_L[g];
+    st4(a.out + b * a.out_bstride + (long long)h * G * D + 4 * tid,
+        make_float4(T.x / Ls, T.y / Ls, T.z / Ls, T.w / Ls));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Split-K decode attention with a reference merge, head_dim 128.
 //
@@ -151,6 +235,8 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   constexpr int NRG = 4 * W;  // row groups
   static_assert(G * D <= kAccL && G <= 4, "accumulator layout holds up to 4 q heads");
+  static_assert(3 * kMaxSplits * G + 4 * 64 * W <= NRG * G * D,
+                "s_o holds the deterministic merge's (m, l), weights and partial sums");
   __shared__ __attribute__((aligned(16))) float s_o[NRG][G][D];
   __shared__ float s_m[NRG][G], s_l[NRG][G], s_w[NRG][G], s_M[G], s_L[G], s_R[G];
   __shared__ unsigned long long s_mk[4];
@@ -333,6 +419,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     if (a.done) signal_host(a.done + b * a.n_kv + h, a.seq);
   };
   const int gs = a.split_off[b] + s;  // global split index
+  const bool det = a.merge_det != 0;
   float *acc = a.acc + ((long long)b * a.n_kv + h) * kAccStride;
   if (!exact) {
     for (int e = tid; e < G * D; e += 64 * W) {
@@ -345,6 +432,8 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
 #pragma unroll
         for (int r = 1; r < NRG; ++r) Ls += s_l[r][g];
         a.out[b * a.out_bstride + (long long)h * G * D + e] = O / Ls;
+      } else if (det) {
+        st_agent(&a.ws_o[((long long)gs * a.n_kv + h) * G * D + e], O);
       } else {
         add_agent(acc + e, O);
       }
@@ -358,7 +447,13 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       float Ls = s_l[0][tid];
 #pragma unroll
       for (int r = 1; r < NRG; ++r) Ls += s_l[r][tid];
-      add_agent(acc + kAccL + tid, Ls);
+      if (det) {
+        float *ml = reinterpret_cast<float *>(&a.ws_ml[((long long)gs * a.n_kv + h) * G + tid]);
+        st_agent(ml, R[tid]);
+        st_agent(ml + 1, Ls);
+      } else {
+        add_agent(acc + kAccL + tid, Ls);
+      }
     }
   } else {
     // ---- exact path: the rows again, a running maximum per row group ----
@@ -431,7 +526,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
       st_agent(ml, s_M[tid]);
       st_agent(ml + 1, s_L[tid]);
     }
-    if (tid == 0) {
+    if (tid == 0 && !det) {
       unsigned long long *mask = reinterpret_cast<unsigned long long *>(acc + kAccMask) + (s >> 6);
       (void)__hip_atomic_fetch_or(mask, 1ull << (s & 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -464,7 +559,14 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     return;
   }
   if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
+  if (det) {
+    // s_o is free now: it holds the splits' (m, l) and weights
+    float2 *s_ml = reinterpret_cast<float2 *>(&s_o[0][0][0]);
+    det_merge<G>(a, b, h, nsplit, s_ml, reinterpret_cast<float *>(s_ml + kMaxSplits * G), s_L, tid,
+                 64 * W);
+  } else {
+    ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
+  }
   signal();
 #if defined(BNR_DECODE_TIMELINE)
   __builtin_amdgcn_s_waitcnt(0);  // the output stores have completed

@@ -82,6 +82,10 @@ struct DecodeArgs {
   // workgroup of a (sequence, kv head) divides.  acc: [batch][n_kv] x
   // kAccStride floats, zero between launches.
   int merge_ref;
+  // With merge_ref: every split stores its (m, l, O) and the last workgroup
+  // combines them in a fixed order (det_merge): outputs bit-identical from
+  // run to run, at the cost measured in the design notes.
+  int merge_det;
   float *acc;
   int ref_waves;  // waves per workgroup of the reference-merge kernel: 4 or 8
   int max_splits;                  // largest split count of the launch (grid x)
@@ -120,6 +124,11 @@ constexpr long long kNoAllocScratchBytes = kNoAllocZeroBytes + kNoAllocMlBytes +
 // The scratch's address on `device` (current), set up once per device: its
 // merge state zeroed by a kernel on `s`, then `s` synchronised.
 hipError_t noalloc_scratch(int device, hipStream_t s, void **out);
+// The scratch of `device` serves one (context, stream) pair at a time:
+// true when it is free (it is then claimed) or already held by this pair.
+// A context gives it up when it is destroyed.
+bool noalloc_claim(int device, const void *ctx, const void *stream);
+void noalloc_release(int device, const void *ctx);
 
 // Decode planner inputs: the device and the context's tuning state.
 struct DecodePlanConfig {
@@ -128,7 +137,8 @@ struct DecodePlanConfig {
   int large_wgs;   // launches of at least this many 64-row workgroups use the two-launch merge
   int force_rpg;   // 0, or a fixed rows-per-row-group (tuning)
   int min_passes;  // at least this many passes per split (tuning, default 1)
-  int merge_mode;  // -1: reference merge (default); 0: second kernel; 1: in-kernel ticket; 2: reference merge
+  int merge_mode;  // -1: reference merge (default); 0: second kernel; 1: in-kernel ticket;
+                   // 2: reference merge; 3: reference merge, deterministic (merge_det)
   int split_cost;  // planner cost of one split of the in-kernel merges (ns), -1: the mode's default
   int ref_rows;    // reference merge: rows per split (0: planner decides)
   int ref_waves;   // reference merge, small launches: 4 or 8 waves per workgroup, or 0:

@@ -26,8 +26,35 @@ __global__ __launch_bounds__(256) void zero_words_kernel(unsigned *p, long long 
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void *g_ptr[kMaxDevices] = {};
+// The (context, stream) pair whose launches use a device's scratch: every
+// launch on one GPU shares the array, so launches from another context or
+// stream could overlap with them on the GPU and race on the accumulators
+// and tickets.
+struct Owner {
+  const void *ctx = nullptr;
+  const void *stream = nullptr;
+};
+Owner g_owner[kMaxDevices];
 
 }  // namespace
+
+bool noalloc_claim(int device, const void *ctx, const void *stream) {
+  if (device < 0 || device >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lk(g_mu);
+  Owner &o = g_owner[device];
+  if (!o.ctx) {
+    o.ctx = ctx;
+    o.stream = stream;
+    return true;
+  }
+  return o.ctx == ctx && o.stream == stream;
+}
+
+void noalloc_release(int device, const void *ctx) {
+  if (device < 0 || device >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_owner[device].ctx == ctx) g_owner[device] = Owner{};
+}
 
 hipError_t noalloc_scratch(int device, hipStream_t s, void **out) {
   *out = nullptr;

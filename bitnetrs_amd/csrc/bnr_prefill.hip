@@ -454,11 +454,13 @@ void prefill_persistent_kernel(PrefillArgs a) {
 // launch finish together, with no tail of short items.  A workgroup's run
 // is a sequence of segments: the key tiles of one query tile that fall in
 // the run.  A segment holding a whole query tile writes its output; the
-// others store their partial state -- slot 2w for the run's first segment,
-// 2w+1 for its last -- and take the query tile's ticket, and the last of
-// its parts (workgroups wf..wl, one segment each) merges the others.  As in
-// the persistent kernel, the next segment's first K/V tile and Q fragment
-// are loaded during the current segment's last tile.
+// others store their partial state with plain stores -- slot 2w for the
+// run's first segment, 2w+1 for its last -- and a second, short launch
+// (prefill_sk_merge_kernel) merges the parts of each split query tile: its
+// workgroup finds the parts' workgroups wf..wl with sk_wg_of and reads
+// their slots.  No tickets or counters are involved.  As in the persistent
+// kernel, the next segment's first K/V tile and Q fragment are loaded
+// during the current segment's last tile.
 //
 // Workgroup index -> run: runs go to the XCDs in blocks (XCD x, which gets
 // workgroups x, x+8, ..., runs the x-th eighth of the units), so that one

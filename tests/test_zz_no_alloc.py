@@ -90,3 +90,71 @@ def test_noalloc_limits_are_errors():
             be.dev_decode_attention_noalloc(z[:8 * D], z, z, 16, out[:8 * D], 8, 2, D, 16)
     finally:
         be.close()
+
+
+def test_noalloc_exact_path_then_plain():
+    """The exact path through the scratch: planted rows score ~130 log2 units
+    above the rest of their split (two heads), and in a third head the newest
+    row points away from q, so every split of that head is flagged; the
+    partial states and masks live in the scratch's ws_ml / ws_o regions.  A
+    plain call follows on the same scratch (masks cleared by the first)."""
+    import torch
+
+    import bitnetrs_amd
+
+    be = bitnetrs_amd.HipBackend(0)
+    try:
+        g = HQ // HKV
+        w = decode_workload(92, 4095, cap=4096, q_scale=1.0)
+        q = w["q"].reshape(HQ, D)
+        for head, rows in [(0, [100, 2500]), (3, [4000])]:
+            for t in rows:
+                w["k_cache"][head, t] = (8.0 * q[head * g]).astype(f32)
+        w["k_cache"][:, w["pos"]] = w["k"].reshape(HKV, D)
+        w["v_cache"][:, w["pos"]] = w["v"].reshape(HKV, D)
+        w["k_cache"][1, w["pos"]] = (-8.0 * q[1 * g]).astype(f32)  # newest row away from q
+        plain = decode_workload(93, 1500, cap=4096)
+        plain["k_cache"][:, plain["pos"]] = plain["k"].reshape(HKV, D)
+        plain["v_cache"][:, plain["pos"]] = plain["v"].reshape(HKV, D)
+        for i, ww in enumerate([w, plain]):
+            case(f"no-alloc exact path: call {i} pos {ww['pos']}")
+            out = torch.zeros(HQ * D, device="cuda")
+            be.dev_decode_attention_noalloc(dev(ww["q"]), dev(ww["k_cache"]), dev(ww["v_cache"]), 4096,
+                                            out, HQ, HKV, D, ww["pos"])
+            torch.cuda.synchronize()
+            assert_close_scaled(out.cpu().numpy(), oracle_attention(ww, HQ, HKV), f"call {i} vs oracle")
+    finally:
+        be.close()
+
+
+def test_noalloc_scratch_has_one_owner():
+    """The per-GPU scratch serves one (context, stream) pair: another context,
+    or the owner on another stream, gets BackendError until the owner is
+    destroyed; then the other context can claim it."""
+    import torch
+
+    import bitnetrs_amd
+
+    w = decode_workload(94, 300, cap=512)
+    w["k_cache"][:, w["pos"]] = w["k"].reshape(HKV, D)
+    w["v_cache"][:, w["pos"]] = w["v"].reshape(HKV, D)
+    q, kc, vc = dev(w["q"]), dev(w["k_cache"]), dev(w["v_cache"])
+    out = torch.zeros(HQ * D, device="cuda")
+    a, b = bitnetrs_amd.HipBackend(0), bitnetrs_amd.HipBackend(0)
+    side = torch.cuda.Stream()
+    try:
+        case("no-alloc scratch owner")
+        a.dev_decode_attention_noalloc(q, kc, vc, 512, out, HQ, HKV, D, w["pos"])
+        with pytest.raises(bitnetrs_amd.BackendError):
+            b.dev_decode_attention_noalloc(q, kc, vc, 512, out, HQ, HKV, D, w["pos"])
+        with pytest.raises(bitnetrs_amd.BackendError):
+            a.dev_decode_attention_noalloc(q, kc, vc, 512, out, HQ, HKV, D, w["pos"], stream=side)
+        a.dev_decode_attention_noalloc(q, kc, vc, 512, out, HQ, HKV, D, w["pos"])  # still the owner
+        torch.cuda.synchronize()
+        a.close()
+        b.dev_decode_attention_noalloc(q, kc, vc, 512, out, HQ, HKV, D, w["pos"])  # released
+        torch.cuda.synchronize()
+        assert_close_scaled(out.cpu().numpy(), oracle_attention(w, HQ, HKV), "new owner vs oracle")
+    finally:
+        a.close()
+        b.close()
