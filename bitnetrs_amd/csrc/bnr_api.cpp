@@ -164,6 +164,7 @@ constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
   int n_tokens, start_pos, n_kv, tiles, balanced;
+  long long cap;
 };
 
 struct DeviceGuard {
@@ -497,175 +498,22 @@ void free_ws(DecodeWs &w) {
 // the library's own stream, the device entry points on the caller's.
 DecodeWs &ws_for(bnr_ctx *c, hipStream_t s) { return s == c->stream ? c->hws : c->dws; }
 
-// Prefill key-range chunking.  The planner replays the launch's dispatch for
-// each candidate chunk size and keeps the shortest span.  Workgroups go to
-// the XCDs round-robin (WG i to XCD i % 8), so one XCD sees every 8th
-// workgroup of the dispatch order and the XCDs finish together; the replay
-// follows XCD 0 alone.  An XCD places a workgroup on a CU with a free slot
-// (two per CU at this kernel's register and LDS use), an idle CU first, and
-// a CU's workgroups share it: one alone runs a 32-key tile in time 1, two
-// side by side each take kShared.  A workgroup's work is its key tiles plus
-// a fixed cost (queries and first tile loaded, outputs stored), plus a
-// partial-state store when its query tile is split; the last chunk of a
-// split tile then reads the others' partials.  The items come in the
-// kernel's order (prefill_map, or pf_bal_map for balanced chunks).  The constants are fitted to measured
-// MI355X spans over 15 shapes x 6 chunk sizes (128 to 8192 tokens, start
-// 0 to 4000; a tile of 4 heads alone on a CU takes about 4 us): they keep
-// the chosen chunk size within 10 % of the best measured one (2 % median).
-double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu,
-                    bool balanced) {
-  constexpr double kShared = 1.9, kFixed = 1.0, kStore = 0.0, kMerge = 0.1;
-  constexpr int kXcd = 8, kSlots = 2;
-  const int ncu = std::max(1, n_cu / kXcd);
-  struct Cu {
-    int n = 0;           // active workgroups
-    double rem[kSlots];  // remaining work of each
-    double tail[kSlots]; // merge work after it (split tiles)
-    double t = 0.0;      // time rem[] refers to
-    unsigned ver = 0;    // bumped whenever the finish times change
-  };
-  struct Ev {
-    double t;
-    int cu;
-    unsigned ver;
-    bool operator<(const Ev &o) const { return t > o.t; }  // min-heap
-  };
-  std::vector<Cu> cus((size_t)ncu);
-  std::vector<Ev> heap;
-  heap.reserve(256);
-  auto rate = [](int n) { return n == 1 ? 1.0 : 1.0 / kShared; };
-  auto advance = [&](Cu &c, double now) {
-    const double r = rate(c.n);
-    for (int i = 0; i < c.n; ++i) c.rem[i] -= (now - c.t) * r;
-    c.t = now;
-  };
-  auto schedule = [&](int cu) {
-    Cu &c = cus[(size_t)cu];
-    ++c.ver;
-    if (c.n == 0) return;
-    double r = c.rem[0];
-    for (int i = 1; i < c.n; ++i) r = std::min(r, c.rem[i]);
-    heap.push_back(Ev{c.t + std::max(r, 0.0) / rate(c.n), cu, c.ver});
-    std::push_heap(heap.begin(), heap.end());
-  };
-  // Free slot on the XCD: an idle CU first, else one running a single workgroup.
-  auto pick = [&]() {
-    int best = -1;
-    for (int i = 0; i < ncu; ++i) {
-      if (cus[(size_t)i].n == 0) return i;
-      if (best < 0 && cus[(size_t)i].n < kSlots) best = i;
-    }
-    return best;
-  };
-
-  const int last_row = start_pos + n_tokens - 1;
-  PrefillArgs order{};
-  order.n_tokens = n_tokens;
-  order.start_pos = start_pos;
-  order.n_qtiles = (n_tokens + 31) / 32;
-  order.chunk_tiles = std::min(std::max(ctiles_in, 1), kPrefillNoSplit);
-  order.balanced = balanced;
-  prefill_order(order);
-  const int ctiles = order.chunk_tiles;
-  const int n_items = prefill_plan(n_tokens, start_pos, ctiles).n_items;
-  double now = 0.0, span = 0.0;
-  long long wg = 0;
-  for (int y = 0; y < n_items; ++y) {
-    int qt, ch, nch, base, t;
-    if (order.balanced) {
-      pf_bal_map(order, y, qt, ch, nch);
-      int kt0;
-      pf_bal_range(std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1, nch, ch, kt0, t);
-    } else {
-      prefill_map(order, y, qt, ch, nch, base);
-      const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
-      t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
-    }
-    {
-      for (int h = 0; h < n_kv; ++h, ++wg) {
-        if (wg % kXcd != 0) continue;
-        int cu;
-        while ((cu = pick()) < 0) {  // wait for a slot: run to the next finish
-          std::pop_heap(heap.begin(), heap.end());
-          const Ev ev = heap.back();
-          heap.pop_back();
-          Cu &c = cus[(size_t)ev.cu];
-          if (ev.ver != c.ver) continue;
-          now = ev.t;
-          advance(c, now);
-          for (int i = 0; i < c.n;) {
-            if (c.rem[i] <= 1e-9) {
-              span = std::max(span, now + c.tail[i]);
-              c.rem[i] = c.rem[c.n - 1];
-              c.tail[i] = c.tail[c.n - 1];
-              --c.n;
-            } else {
-              ++i;
-            }
-          }
-          schedule(ev.cu);
-        }
-        Cu &c = cus[(size_t)cu];
-        advance(c, now);
-        c.rem[c.n] = kFixed + t + (nch > 1 ? kStore : 0.0);
-        c.tail[c.n] = nch > 1 ? (nch - 1) * kMerge : 0.0;
-        ++c.n;
-        schedule(cu);
-      }
-    }
-  }
-  for (Cu &c : cus) {  // drain
-    const double r = rate(c.n);
-    for (int i = 0; i < c.n; ++i) {
-      // the shorter of two shared workgroups ends first, the other then runs alone
-      double end;
-      if (c.n == 2) {
-        const double a = std::min(c.rem[0], c.rem[1]), b = std::max(c.rem[0], c.rem[1]);
-        end = c.t + (c.rem[i] == a ? a / r : a / r + (b - a));
-      } else {
-        end = c.t + c.rem[i] / r;
-      }
-      span = std::max(span, end + c.tail[i]);
-    }
-  }
-  return span;
-}
-
-// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split), and
-// whether the chunks are balanced (*balanced); the last 16 shapes are
-// remembered, a new one costs two replays per candidate (tens to hundreds
-// of us each).  Sizes between the powers of two matter:
-// they set how evenly the items fill the resident slots (N = 1024 runs 8 %
-// faster at 6 tiles than at 4, 512 queries after 1536 cached 14 % faster at
-// 10 than at 4 or 16).
-constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
-constexpr long long kPrefillMaxSplitItems = 8192;  // (kv head, item) pairs of a planned split
-
-int plan_prefill_chunk(bnr_ctx *c, int n_tokens, int start_pos, int n_kv, int *balanced) {
+// The planner's chunk size for a prefill shape, remembered for the last 16
+// shapes (planning replays the dispatch for every candidate).
+int plan_prefill_cached(bnr_ctx *c, int n_tokens, int start_pos, int n_kv, long long cap,
+                        int *balanced) {
   for (const PrefillPlanEntry &e : c->pf_plans)
-    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv) {
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv && e.cap == cap) {
       *balanced = e.balanced;
       return e.tiles;
     }
-  int best = kPrefillNoSplit, best_bal = 0;
-  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, c->n_cu, false);
-  for (int ct : kPrefillChunkCandidates) {
-    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > kPrefillMaxSplitItems)
-      continue;
-    for (int bal = 0; bal <= 1; ++bal) {
-      if ((bal == 0 && c->pf_balanced == 1) || (bal == 1 && c->pf_balanced == 0)) continue;
-      const double span = prefill_span(n_tokens, start_pos, n_kv, ct, c->n_cu, bal != 0);
-      if (span < best_span * 0.99) {
-        best_span = span;
-        best = ct;
-        best_bal = bal;
-      }
-    }
-  }
+  int bal = 0;
+  const int tiles =
+      plan_prefill_chunk(n_tokens, start_pos, n_kv, c->n_cu, c->pf_balanced, cap, &bal);
   if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
-  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, best, best_bal});
-  *balanced = best_bal;
-  return best;
+  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, tiles, bal, cap});
+  *balanced = bal;
+  return tiles;
 }
 
 // RopeCache::new (bitnet-cpu/src/rope.rs:100-153) on the host: same f32
@@ -1856,7 +1704,8 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
       int bal = c->pf_balanced == 1;
       pa.chunk_tiles = c->pf_chunk_tiles > 0
                            ? c->pf_chunk_tiles
-                           : plan_prefill_chunk(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads, &bal);
+                           : plan_prefill_cached(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads,
+                                                 (long long)cap, &bal);
       pa.balanced = bal;
     } else {
       pa.chunk_tiles = kPrefillNoSplit;
@@ -1870,15 +1719,14 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
       // Partial states and tickets, sized -- whatever this launch needs --
       // for every launch on a cache of `cap` rows, so that later calls on it
       // (also under HIP graph capture) never allocate: stream-K launches keep
-      // two states per resident workgroup; chunked launches at most T =
-      // cap/32 query tiles of at most ceil(T / chunk) chunks each, and at
-      // most kPrefillMaxSplitItems (kv head, item) pairs when the planner
-      // chooses the chunk (a forced chunk size sets its own bound).
+      // two states per resident workgroup; a planned chunk size keeps to
+      // prefill_item_budget (kv head, item) pairs; a forced one (tuning) to
+      // T = cap/32 query tiles of at most ceil(T / chunk) chunks each.
       const long long T = ((long long)cap + 31) / 32;
-      const long long ct = c->pf_chunk_tiles > 0 ? pa.chunk_tiles : kPrefillChunkCandidates[0];
-      long long items = (long long)n_kv_heads * T * ((T + ct - 1) / ct);
-      if (c->pf_chunk_tiles <= 0) items = std::min<long long>(items, kPrefillMaxSplitItems);
-      items = std::max<long long>(items, (long long)n_kv_heads * plan.n_items);
+      long long items = c->pf_chunk_tiles > 0
+                            ? (long long)n_kv_heads * T * ((T + pa.chunk_tiles - 1) / pa.chunk_tiles)
+                            : prefill_item_budget((long long)cap, (int)n_kv_heads);
+      if (plan.split) items = std::max<long long>(items, (long long)n_kv_heads * plan.n_items);
       items = std::max<long long>(items, 2LL * c->n_cu * per_cu);
       st = ensure_buf(&c->pf_ws, &c->pf_ws_floats, (size_t)items * group * 66 * 64,
                       "prefill workspace alloc");

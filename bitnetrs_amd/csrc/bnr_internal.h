@@ -405,6 +405,15 @@ PrefillPlan prefill_plan(int n_tokens, int start_pos, int chunk_tiles);
 // chunks need 1 < chunk_tiles <= kMaxLptChunk; otherwise a.balanced is
 // cleared.
 void prefill_order(PrefillArgs &a);
+// Chunk planning (bnr_prefill_plan.cpp).  prefill_span: modelled span of a
+// launch at ctiles key tiles per chunk.  plan_prefill_chunk: the planner's
+// key tiles per chunk (kPrefillNoSplit: none) and *balanced for one shape,
+// among the candidates that fit prefill_item_budget(cap, n_kv).
+double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles, int n_cu, bool balanced);
+int plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
+                       long long cap, int *balanced);
+long long prefill_item_budget(long long cap, int n_kv);
+constexpr long long kPrefillMaxPlannedItems = 8192;
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.
 // Stream-K runs: workgroup w of P takes units [sk_u0(w), sk_u0(w + 1)), a
 // sequence of segments (the key tiles of one query tile within the run).

@@ -1,0 +1,192 @@
+// Host-side planning of chunked prefill launches: the dispatch replay that
+// scores a key-chunk size, the planner that picks one per launch shape, and
+// the bound on the partial-state workspace those picks can need on a cache
+// of a given capacity.  Pure functions of the shape and the CU count; no
+// GPU is touched, so host-only checks link them directly.
+#include <algorithm>
+#include <vector>
+
+#include "bnr_internal.h"
+
+namespace bnr {
+
+// Prefill key-range chunking.  The planner replays the launch's dispatch for
+// each candidate chunk size and keeps the shortest span.  Workgroups go to
+// the XCDs round-robin (WG i to XCD i % 8), so one XCD sees every 8th
+// workgroup of the dispatch order and the XCDs finish together; the replay
+// follows XCD 0 alone.  An XCD places a workgroup on a CU with a free slot
+// (two per CU at this kernel's register and LDS use), an idle CU first, and
+// a CU's workgroups share it: one alone runs a 32-key tile in time 1, two
+// side by side each take kShared.  A workgroup's work is its key tiles plus
+// a fixed cost (queries and first tile loaded, outputs stored), plus a
+// partial-state store when its query tile is split; the last chunk of a
+// split tile then reads the others' partials.  The items come in the
+// kernel's order (prefill_map, or pf_bal_map for balanced chunks).  The constants are fitted to measured
+// MI355X spans over 15 shapes x 6 chunk sizes (128 to 8192 tokens, start
+// 0 to 4000; a tile of 4 heads alone on a CU takes about 4 us): they keep
+// the chosen chunk size within 10 % of the best measured one (2 % median).
+double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu,
+                    bool balanced) {
+  constexpr double kShared = 1.9, kFixed = 1.0, kStore = 0.0, kMerge = 0.1;
+  constexpr int kXcd = 8, kSlots = 2;
+  const int ncu = std::max(1, n_cu / kXcd);
+  struct Cu {
+    int n = 0;           // active workgroups
+    double rem[kSlots];  // remaining work of each
+    double tail[kSlots]; // merge work after it (split tiles)
+    double t = 0.0;      // time rem[] refers to
+    unsigned ver = 0;    // bumped whenever the finish times change
+  };
+  struct Ev {
+    double t;
+    int cu;
+    unsigned ver;
+    bool operator<(const Ev &o) const { return t > o.t; }  // min-heap
+  };
+  std::vector<Cu> cus((size_t)ncu);
+  std::vector<Ev> heap;
+  heap.reserve(256);
+  auto rate = [](int n) { return n == 1 ? 1.0 : 1.0 / kShared; };
+  auto advance = [&](Cu &c, double now) {
+    const double r = rate(c.n);
+    for (int i = 0; i < c.n; ++i) c.rem[i] -= (now - c.t) * r;
+    c.t = now;
+  };
+  auto schedule = [&](int cu) {
+    Cu &c = cus[(size_t)cu];
+    ++c.ver;
+    if (c.n == 0) return;
+    double r = c.rem[0];
+    for (int i = 1; i < c.n; ++i) r = std::min(r, c.rem[i]);
+    heap.push_back(Ev{c.t + std::max(r, 0.0) / rate(c.n), cu, c.ver});
+    std::push_heap(heap.begin(), heap.end());
+  };
+  // Free slot on the XCD: an idle CU first, else one running a single workgroup.
+  auto pick = [&]() {
+    int best = -1;
+    for (int i = 0; i < ncu; ++i) {
+      if (cus[(size_t)i].n == 0) return i;
+      if (best < 0 && cus[(size_t)i].n < kSlots) best = i;
+    }
+    return best;
+  };
+
+  const int last_row = start_pos + n_tokens - 1;
+  PrefillArgs order{};
+  order.n_tokens = n_tokens;
+  order.start_pos = start_pos;
+  order.n_qtiles = (n_tokens + 31) / 32;
+  order.chunk_tiles = std::min(std::max(ctiles_in, 1), kPrefillNoSplit);
+  order.balanced = balanced;
+  prefill_order(order);
+  const int ctiles = order.chunk_tiles;
+  const int n_items = prefill_plan(n_tokens, start_pos, ctiles).n_items;
+  double now = 0.0, span = 0.0;
+  long long wg = 0;
+  for (int y = 0; y < n_items; ++y) {
+    int qt, ch, nch, base, t;
+    if (order.balanced) {
+      pf_bal_map(order, y, qt, ch, nch);
+      int kt0;
+      pf_bal_range(std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1, nch, ch, kt0, t);
+    } else {
+      prefill_map(order, y, qt, ch, nch, base);
+      const int nk = std::min(start_pos + qt * 32 + 31, last_row) / 32 + 1;
+      t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
+    }
+    {
+      for (int h = 0; h < n_kv; ++h, ++wg) {
+        if (wg % kXcd != 0) continue;
+        int cu;
+        while ((cu = pick()) < 0) {  // wait for a slot: run to the next finish
+          std::pop_heap(heap.begin(), heap.end());
+          const Ev ev = heap.back();
+          heap.pop_back();
+          Cu &c = cus[(size_t)ev.cu];
+          if (ev.ver != c.ver) continue;
+          now = ev.t;
+          advance(c, now);
+          for (int i = 0; i < c.n;) {
+            if (c.rem[i] <= 1e-9) {
+              span = std::max(span, now + c.tail[i]);
+              c.rem[i] = c.rem[c.n - 1];
+              c.tail[i] = c.tail[c.n - 1];
+              --c.n;
+            } else {
+              ++i;
+            }
+          }
+          schedule(ev.cu);
+        }
+        Cu &c = cus[(size_t)cu];
+        advance(c, now);
+        c.rem[c.n] = kFixed + t + (nch > 1 ? kStore : 0.0);
+        c.tail[c.n] = nch > 1 ? (nch - 1) * kMerge : 0.0;
+        ++c.n;
+        schedule(cu);
+      }
+    }
+  }
+  for (Cu &c : cus) {  // drain
+    const double r = rate(c.n);
+    for (int i = 0; i < c.n; ++i) {
+      // the shorter of two shared workgroups ends first, the other then runs alone
+      double end;
+      if (c.n == 2) {
+        const double a = std::min(c.rem[0], c.rem[1]), b = std::max(c.rem[0], c.rem[1]);
+        end = c.t + (c.rem[i] == a ? a / r : a / r + (b - a));
+      } else {
+        end = c.t + c.rem[i] / r;
+      }
+      span = std::max(span, end + c.tail[i]);
+    }
+  }
+  return span;
+}
+
+constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
+
+// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split), and
+// whether the chunks are balanced (*balanced).  Each candidate costs two
+// dispatch replays (tens to hundreds of us each); sizes between the powers
+// of two matter: they set how evenly the items fill the resident slots
+// (N = 1024 runs 8 % faster at 6 tiles than at 4, 512 queries after 1536
+// cached 14 % faster at 10 than at 4 or 16).  bal_pref: -1 either, 0 plain
+// chunks only, 1 balanced chunks only.  A candidate whose (kv head, item)
+// pairs would exceed prefill_item_budget(cap) is not considered, so the
+// workspace sized by that budget holds every planned launch.
+int plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
+                       long long cap, int *balanced) {
+  const long long budget = prefill_item_budget(cap, n_kv);
+  int best = kPrefillNoSplit, best_bal = 0;
+  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, n_cu, false);
+  for (int ct : kPrefillChunkCandidates) {
+    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > budget) continue;
+    for (int bal = 0; bal <= 1; ++bal) {
+      if ((bal == 0 && bal_pref == 1) || (bal == 1 && bal_pref == 0)) continue;
+      const double span = prefill_span(n_tokens, start_pos, n_kv, ct, n_cu, bal != 0);
+      if (span < best_span * 0.99) {
+        best_span = span;
+        best = ct;
+        best_bal = bal;
+      }
+    }
+  }
+  *balanced = best_bal;
+  return best;
+}
+
+// (kv head, item) pairs a planned chunked launch may use on a cache of cap
+// rows: four chunks per query tile on average over the cap/32 query tiles,
+// and never more than kPrefillMaxPlannedItems.  Replaying the planner over
+// every 32-aligned (tokens, start) pair a cache of 2048 / 4096 / 8192 rows
+// allows (5 kv heads, start below the token count: the launches that take
+// key chunks), the budget lengthens the modelled span by 0.3 / 1.5 / 1.0 %
+// at worst against unlimited items, 0.0 % on average.  The partial states
+// cost group * 66 * 64 floats (16.9 KB per q head) each.
+long long prefill_item_budget(long long cap, int n_kv) {
+  const long long tiles = (std::max(cap, 1LL) + 31) / 32;
+  return std::min(4LL * n_kv * tiles, kPrefillMaxPlannedItems);
+}
+
+}  // namespace bnr

@@ -27,12 +27,12 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
 
 
-@pytest.mark.parametrize("cap", [1024, 2048])
-def test_prefill_at_capacity_captured(backend, cap):
+@pytest.mark.parametrize("cap,n,start", [(1024, 1024, 0), (2048, 2048, 0), (4096, 1568, 320)])
+def test_prefill_at_capacity_captured(backend, cap, n, start):
     import torch
 
-    case(f"captured prefill N={cap} after a 64-token warm-up")
-    w = prefill_workload(70, cap)
+    case(f"captured prefill N={n} at {start} on cap {cap} after a 64-token warm-up")
+    w = prefill_workload(70, n)
     q0, k0, v = dev(w["q"]), dev(w["k"]), dev(w["v"])
     kc = torch.zeros(HKV, cap, D, device="cuda")
     vc = torch.zeros_like(kc)
@@ -42,18 +42,18 @@ def test_prefill_at_capacity_captured(backend, cap):
     backend.dev_prefill(qw, kw, v[:64], 64, 0, HQ, HKV, D, THETA, kc, vc, cap, ow)
     # captured straight after the warm-up: nothing larger ran on this cache
     q, k = q0.clone(), k0.clone()
-    out = torch.zeros(cap, HQ * D, device="cuda")
+    out = torch.zeros(n, HQ * D, device="cuda")
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         q.copy_(q0)
         k.copy_(k0)
-        backend.dev_prefill(q, k, v, cap, 0, HQ, HKV, D, THETA, kc, vc, cap, out)
+        backend.dev_prefill(q, k, v, n, start, HQ, HKV, D, THETA, kc, vc, cap, out)
     # eager reference of the same call
     qe, ke = q0.clone(), k0.clone()
     out_ref = torch.zeros_like(out)
     kc.zero_()
     vc.zero_()
-    backend.dev_prefill(qe, ke, v, cap, 0, HQ, HKV, D, THETA, kc, vc, cap, out_ref)
+    backend.dev_prefill(qe, ke, v, n, start, HQ, HKV, D, THETA, kc, vc, cap, out_ref)
     torch.cuda.synchronize()
     q_ref, k_ref, kc_ref, vc_ref = qe.clone(), ke.clone(), kc.clone(), vc.clone()
     for r in range(3):
@@ -71,6 +71,47 @@ def test_prefill_at_capacity_captured(backend, cap):
         backend.dev_prefill(qw, kw, v[:64], 64, 0, HQ, HKV, D, THETA, kc, vc, cap, ow)
         torch.cuda.synchronize()
     del g
+
+
+def prefill_workspace_bytes(cap, n_cu, group=HQ // HKV, n_kv=HKV):
+    """Partial states the first prefill on a cache of `cap` rows reserves:
+    the planner's budget of four (kv head, item) pairs per query tile, at
+    most 8192, or two per resident workgroup of a stream-K launch (two per
+    CU below group 8), whichever is more; group * 66 * 64 floats each."""
+    tiles = (cap + 31) // 32
+    per_cu = 1 if group >= 8 else 2
+    items = max(min(4 * n_kv * tiles, 8192), 2 * n_cu * per_cu)
+    return items * group * 66 * 64 * 4
+
+
+@pytest.mark.parametrize("cap", [2048, 8192])
+def test_prefill_workspace_reserved_by_cap(cap):
+    """The first prefill on a cache reserves the workspace every later
+    launch on it can need, and no more: device memory taken by a 64-token
+    prefill in a fresh context is the partial-state workspace for `cap`
+    plus small tables (RoPE rows, tickets)."""
+    import torch
+
+    import bitnetrs_amd
+
+    case(f"prefill workspace reserved for cap {cap}")
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    w = prefill_workload(71, 64)
+    q, k, v = dev(w["q"]), dev(w["k"]), dev(w["v"])
+    kc = torch.zeros(HKV, cap, D, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.zeros(64, HQ * D, device="cuda")
+    be = bitnetrs_amd.HipBackend(0)
+    try:
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        be.dev_prefill(q, k, v, 64, 0, HQ, HKV, D, THETA, kc, vc, cap, out)
+        torch.cuda.synchronize()
+        taken = free0 - torch.cuda.mem_get_info()[0]
+    finally:
+        be.close()
+    want = prefill_workspace_bytes(cap, n_cu)
+    assert want <= taken <= want + (16 << 20), f"cap {cap}: took {taken} B, workspace {want} B"
 
 
 def test_decode_steps_captured_past_warmup(backend):
