@@ -1035,6 +1035,164 @@ def decode_timeline_main(args) -> int:
     return 0
 
 
+# Words of a prefill workgroup's timeline record (PfStamp in bnr_internal.h).
+PF_ENTRY, PF_READY, PF_TILES, PF_TICKET, PF_MERGED, PF_STORED, PF_HWID, PF_ITEM = range(8)
+
+
+def prefill_launch_stats(rows, tick_us):
+    """One launch's records (rows of 8 words, one per workgroup) -> phase
+    statistics in us: span, start latency, per-key-tile time, partial-state
+    store + ticket, merge, output store; per-CU residency and how many
+    workgroups are still running as the launch drains."""
+    import numpy as np
+
+    t0 = rows[:, PF_ENTRY].min()
+    ends = np.maximum.reduce([rows[:, PF_TICKET], rows[:, PF_MERGED], rows[:, PF_STORED]])
+    span = ends.max() - t0
+    ntiles = (rows[:, PF_ITEM] & 0xFFFF).astype(np.float64)
+    nch = (rows[:, PF_ITEM] >> 16) & 0xFFFF
+    split = nch > 1
+    merger = rows[:, PF_MERGED] != 0
+    writer = rows[:, PF_STORED] != 0
+    hw = rows[:, PF_HWID]
+    # XCC_ID, then HW_ID's SE / SH / CU fields (bits 8..15): one CU
+    cu_key = ((hw >> 32) << 8) | ((hw >> 8) & 0xFF)
+    cus = np.unique(cu_key)
+    # per CU: time with >= 1 workgroup in its key-tile phase, mean residents
+    busy, resident = [], []
+    for c in cus:
+        sel = cu_key == c
+        iv = sorted(zip(rows[sel, PF_READY], rows[sel, PF_TILES]))
+        tot, cur_s, cur_e = 0, None, None
+        for a, b in iv:
+            if cur_e is None or a > cur_e:
+                if cur_e is not None:
+                    tot += cur_e - cur_s
+                cur_s, cur_e = a, b
+            else:
+                cur_e = max(cur_e, b)
+        if cur_e is not None:
+            tot += cur_e - cur_s
+        busy.append(tot / span)
+        resident.append((ends[sel] - rows[sel, PF_ENTRY]).sum() / span)
+    rel_end = (ends - t0) / span
+    med = lambda x: float(np.median(x)) if len(x) else 0.0  # noqa: E731
+    out = {
+        "span": span * tick_us,
+        "wgs": int(len(rows)),
+        "cus": int(len(cus)),
+        "entry_spread": (rows[:, PF_ENTRY].max() - t0) * tick_us,
+        "start_latency": med(rows[:, PF_READY] - rows[:, PF_ENTRY]) * tick_us,
+        "start_latency_p90": float(np.percentile(rows[:, PF_READY] - rows[:, PF_ENTRY], 90)) * tick_us,
+        "tile": med((rows[:, PF_TILES] - rows[:, PF_READY]) / ntiles) * tick_us,
+        "key_tiles_mean": float(ntiles.mean()),
+        "ticket": med(rows[split, PF_TICKET] - rows[split, PF_TILES]) * tick_us,
+        "merge": med(rows[merger, PF_MERGED] - rows[merger, PF_TICKET]) * tick_us,
+        "store": med(rows[writer, PF_STORED] - np.maximum(rows[writer, PF_MERGED],
+                                                           rows[writer, PF_TILES])) * tick_us,
+        "cu_tile_busy": med(busy),
+        "cu_residents": med(resident),
+        "first_end": (ends.min() - t0) * tick_us,
+        "end_p50": float(np.percentile(rel_end, 50)) * span * tick_us,
+        "end_p90": float(np.percentile(rel_end, 90)) * span * tick_us,
+    }
+    # workgroups still running at tenths of the span
+    out["running_by_tenth"] = [int(((rows[:, PF_ENTRY] <= t0 + f * span) & (ends > t0 + f * span)).sum())
+                               for f in np.arange(0.0, 1.0, 0.1)]
+    return out, t0, ends.max()
+
+
+def prefill_timeline_main(args) -> int:
+    """Per-workgroup timeline of the grid-mapped prefill kernel on the
+    30-layer stack's prefill (N = --prefill-tokens from an empty cache of
+    N + 256 rows, RoPE + append + attention per layer, the planner's chunks)
+    as a HIP graph of 30 layers' launches replayed --replays times (q and k
+    restored between replays, untimed).  Loads the measurement build
+    libbitnet_hip_timeline.so, whose prefill kernel stores eight words per
+    workgroup (PfStamp).  Prints one JSON line of medians over launches."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from bitnetrs_amd import _lib
+
+    path = os.path.join(ROOT, "bitnetrs_amd", "libbitnet_hip_timeline.so")
+    if not os.path.exists(path):
+        log("libbitnet_hip_timeline.so is not built (make -C bitnetrs_amd/csrc)")
+        return 1
+    _lib.LIB_PATH = path
+    import bitnetrs_amd
+
+    lib = _lib.load()
+    lib.bnr_debug_decode_timeline.restype = ctypes.c_int
+    lib.bnr_debug_decode_timeline.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    be = bitnetrs_amd.HipBackend(0)
+    log(f"device: {be.device_name()} (timeline build)")
+    n_layers, n = 30, args.prefill_tokens
+    cap, reps = n + 256, args.replays
+    g = torch.Generator(device="cuda").manual_seed(0xB17E7050)
+    qp = torch.randn(n_layers, n, HQ * D, device="cuda", generator=g)
+    kp = torch.randn(n_layers, n, HKV * D, device="cuda", generator=g)
+    vp = torch.randn(n_layers, n, HKV * D, device="cuda", generator=g)
+    kc = torch.zeros(n_layers, HKV, cap, D, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.zeros_like(qp)
+    q_in, k_in = qp.clone(), kp.clone()
+    max_wg = 8192
+    stamps = torch.zeros(n_layers, max_wg * 8, dtype=torch.int64, device="cuda")
+
+    def layer(i, rec=True):
+        _lib.check(lib.bnr_debug_decode_timeline(be._h, stamps[i].data_ptr() if rec else None))
+        be.dev_prefill(qp[i], kp[i], vp[i], n, 0, HQ, HKV, D, THETA, kc[i], vc[i], cap, out[i])
+
+    layer(0, rec=False)  # sizes the table and workspace
+    torch.cuda.synchronize()
+    qp.copy_(q_in)
+    kp.copy_(k_in)
+    graph = capture(torch, layer, n_layers)
+    _lib.check(lib.bnr_debug_decode_timeline(be._h, None))
+    tick_us = 1.0 / 100.0
+    t0e = torch.cuda.Event(enable_timing=True)
+    t1e = torch.cuda.Event(enable_timing=True)
+    samples, gaps, per_layer = [], [], []
+    for r in range(reps):
+        qp.copy_(q_in)
+        kp.copy_(k_in)
+        stamps.zero_()
+        torch.cuda.synchronize()
+        t0e.record()
+        graph.replay()
+        t1e.record()
+        torch.cuda.synchronize()
+        per_layer.append(t0e.elapsed_time(t1e) / n_layers)
+        st = stamps.cpu().numpy().reshape(n_layers, max_wg, 8)
+        bounds = []
+        for i in range(n_layers):
+            rows = st[i][st[i][:, PF_ENTRY] != 0]
+            stats, first, last = prefill_launch_stats(rows, tick_us)
+            samples.append(stats)
+            bounds.append((first, last))
+        gaps += [(bounds[i + 1][0] - bounds[i][1]) * tick_us for i in range(n_layers - 1)]
+    med = lambda xs: float(np.median(xs))  # noqa: E731
+    flops = prefill_flops(n)
+    res = {"workload": f"bitnet_2b_attention_stack_30L_prefill{n}_fp32 (timeline build)",
+           "launches": len(samples), "replays": reps,
+           "graph_layer_us": round(med(per_layer) * 1e3, 3),
+           "graph_layer_tflops": round(flops / (med(per_layer) * 1e-3) / 1e12, 2),
+           "gap_to_next_launch_us": round(med(gaps), 3)}
+    for key in samples[0]:
+        if key == "running_by_tenth":
+            res[key] = [int(np.median([x[key][j] for x in samples])) for j in range(10)]
+        else:
+            res[key if key in ("wgs", "cus", "key_tiles_mean", "cu_tile_busy", "cu_residents")
+                else key + "_us"] = round(med([x[key] for x in samples]), 3)
+    res["span_tflops"] = round(flops / (res["span_us"] * 1e-6) / 1e12, 2)
+    print(json.dumps(res), flush=True)
+    be.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -1066,6 +1224,9 @@ def main() -> int:
     ap.add_argument("--decode-timeline", action="store_true",
                     help="only the per-phase timeline of the decode kernel (loads the "
                          "measurement build libbitnet_hip_timeline.so)")
+    ap.add_argument("--prefill-timeline", action="store_true",
+                    help="only the per-workgroup timeline of the stack-shape prefill (loads the "
+                         "measurement build libbitnet_hip_timeline.so; --prefill-tokens sets N)")
     ap.add_argument("--no-parity", action="store_true",
                     help="skip the oracle checks of the timed outputs")
     args = ap.parse_args()
@@ -1077,6 +1238,8 @@ def main() -> int:
 
     if args.decode_timeline:
         return decode_timeline_main(args)
+    if args.prefill_timeline:
+        return prefill_timeline_main(args)
 
     import torch
 

@@ -261,8 +261,8 @@ struct bnr_ctx {
   int ref_rows = 0;     // reference merge: rows per split (0: planner)
   int ref_waves = 0;    // reference merge, small launches: 4 or 8 waves, 0: by length
 
-  // measurement builds (BNR_DECODE_TIMELINE): where decode launches store
-  // their phase stamps (bnr_debug_decode_timeline), or null
+  // measurement builds (BNR_TIMELINE): where decode and grid-mapped prefill
+  // launches store their phase stamps (bnr_debug_decode_timeline), or null
   unsigned long long *timeline = nullptr;
 
   // device scratch of bnr_dev_decode_attention_noalloc (this GPU's copy)
@@ -1411,11 +1411,11 @@ extern "C" int bnr_dev_stream_read(bnr_ctx *c, const void *a, size_t a_bytes, co
   return set_ok();
 }
 
-#if defined(BNR_DECODE_TIMELINE)
-// Measurement builds only (not in the public header): the next decode
-// launches of this context store kTimelineStamps stamps per workgroup at
-// `stamps` (device memory, 8 bytes each, one slot per workgroup of the grid;
-// null: none).
+#if defined(BNR_TIMELINE)
+// Measurement builds only (not in the public header): the next decode and
+// grid-mapped prefill launches of this context store kTimelineStamps stamps
+// per workgroup at `stamps` (device memory, 8 bytes each, one slot per
+// workgroup of the grid; null: none).
 extern "C" int bnr_debug_decode_timeline(bnr_ctx *c, void *stamps) {
   if (!c) return err_backend("context is NULL");
   c->timeline = static_cast<unsigned long long *>(stamps);
@@ -1657,28 +1657,39 @@ extern "C" int bnr_dev_decode_step_batched(bnr_ctx *c, const float *q, const flo
   return set_ok();
 }
 
-extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float *k_cache,
-                                         const float *v_cache, size_t cap, float *out,
-                                         size_t n_tokens, size_t start_pos, size_t n_heads,
-                                         size_t n_kv_heads, size_t head_dim, void *stream) {
-  if (!c) return err_backend("context is NULL");
-  int st = check_heads(n_heads, n_kv_heads, head_dim);
-  if (st) return st;
-  if (n_tokens == 0) return set_ok();
-  st = check_rows(start_pos + n_tokens - 1, cap);
-  if (st) return st;
-  if (!q || !k_cache || !v_cache || !out) return err_backend("prefill_attention: NULL pointer");
-  std::lock_guard<std::mutex> lk(c->mu);
-  DeviceGuard dg(c->device);
-  hipStream_t s = (hipStream_t)stream;
+namespace {
+
+// Whether prefill attention of this shape runs the tiled kernels.  They take
+// at most 65535 query tiles (the grid's y extent) and int positions; longer
+// launches run as per-row decodes.
+bool prefill_tiled(size_t n_tokens, size_t start_pos, size_t n_heads, size_t n_kv_heads,
+                   size_t head_dim, const void *q, const void *k_cache, const void *v_cache,
+                   const void *out) {
+  return head_dim == (size_t)kHeadDim && prefill_supported((int)(n_heads / n_kv_heads)) &&
+         aligned16(q) && aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
+         n_tokens <= (size_t)kPrefillMaxTokens && start_pos + n_tokens <= (size_t)INT32_MAX;
+}
+
+// Stream-K where every query tile has about as many keys as the next (a
+// cached prefix at least as long as the new tokens: 512 queries after 1536
+// cached rows 98 vs 100 us, 1024 after 3000 303 vs 312 us on MI355X);
+// planned key chunks otherwise (N = 1024 from an empty cache: 73 vs 85 us,
+// N = 4096: 676 vs 710 us).
+bool prefill_streamk(const bnr_ctx *c, size_t n_tokens, size_t start_pos) {
+  return c->pf_chunk_tiles <= 0 &&
+         (c->pf_mode == kPrefillStreamK || (c->pf_mode == kPrefillAuto && start_pos >= n_tokens));
+}
+
+// Prefill attention with c->mu held.
+int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
+                             const float *v_cache, size_t cap, float *out, size_t n_tokens,
+                             size_t start_pos, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                             hipStream_t s) {
+  int st = BNR_OK;
   const long long qs = (long long)(n_heads * head_dim);
   const long long kv_stride = (long long)(cap * head_dim);
   const int group = (int)(n_heads / n_kv_heads);
-  // The tiled kernel takes at most 65535 query tiles (its grid's y extent)
-  // and int positions; longer launches run as per-row decodes below.
-  if (head_dim == (size_t)kHeadDim && prefill_supported(group) && aligned16(q) &&
-      aligned16(k_cache) && aligned16(v_cache) && aligned16(out) &&
-      n_tokens <= (size_t)kPrefillMaxTokens && start_pos + n_tokens <= (size_t)INT32_MAX) {
+  if (prefill_tiled(n_tokens, start_pos, n_heads, n_kv_heads, head_dim, q, k_cache, v_cache, out)) {
     PrefillArgs pa{};
     pa.q = q;
     pa.k_cache = k_cache;
@@ -1691,15 +1702,9 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
     pa.n_kv = (int)n_kv_heads;
     pa.scale_log2 = 1.4426950408889634f / sqrtf((float)kHeadDim);
     pa.n_qtiles = (int)((n_tokens + 31) / 32);
+    pa.timeline = c->timeline;
     const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
-    // Stream-K where every query tile has about as many keys as the next
-    // (a cached prefix at least as long as the new tokens: 512 queries after
-    // 1536 cached rows 98 vs 100 us, 1024 after 3000 303 vs 312 us on
-    // MI355X); planned key chunks otherwise (N = 1024 from an empty cache:
-    // 73 vs 85 us, N = 4096: 676 vs 710 us).
-    const bool streamk = c->pf_chunk_tiles <= 0 &&
-                         (c->pf_mode == kPrefillStreamK ||
-                          (c->pf_mode == kPrefillAuto && start_pos >= n_tokens));
+    const bool streamk = prefill_streamk(c, n_tokens, start_pos);
     if (!streamk) {
       int bal = c->pf_balanced == 1;
       pa.chunk_tiles = c->pf_chunk_tiles > 0
@@ -1788,15 +1793,52 @@ extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float
   return set_ok();
 }
 
+}  // namespace
+
+extern "C" int bnr_dev_prefill_attention(bnr_ctx *c, const float *q, const float *k_cache,
+                                         const float *v_cache, size_t cap, float *out,
+                                         size_t n_tokens, size_t start_pos, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, void *stream) {
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (st) return st;
+  if (n_tokens == 0) return set_ok();
+  st = check_rows(start_pos + n_tokens - 1, cap);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !out) return err_backend("prefill_attention: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  st = prefill_attention_locked(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
+                                n_kv_heads, head_dim, (hipStream_t)stream);
+  return st ? st : set_ok();
+}
+
+// bnr_dev_rope_append then bnr_dev_prefill_attention under one lock: the
+// first's checks, then the output pointer's.
 extern "C" int bnr_dev_prefill(bnr_ctx *c, float *q, float *k, const float *v, size_t n_tokens,
                                size_t start_pos, size_t n_heads, size_t n_kv_heads,
                                size_t head_dim, float theta, float *k_cache, float *v_cache,
                                size_t cap, float *out, void *stream) {
-  int st = bnr_dev_rope_append(c, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
-                               theta, k_cache, v_cache, cap, stream);
+  if (!c) return err_backend("context is NULL");
+  int st = check_heads(n_heads, n_kv_heads, head_dim);
+  if (!st) st = check_rope(head_dim, theta);
   if (st) return st;
-  return bnr_dev_prefill_attention(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
-                                   n_kv_heads, head_dim, stream);
+  if (n_tokens == 0) return set_ok();
+  st = check_rows(start_pos + n_tokens - 1, cap);
+  if (st) return st;
+  if (!q || !k || !v || !k_cache || !v_cache) return err_backend("rope_append: NULL pointer");
+  if (!out) return err_backend("prefill_attention: NULL pointer");
+  std::lock_guard<std::mutex> lk(c->mu);
+  DeviceGuard dg(c->device);
+  hipStream_t s = (hipStream_t)stream;
+  st = ensure_table(c, std::max(start_pos + n_tokens, cap) - 1, head_dim, theta);
+  if (st) return st;
+  st = launch_rope_append_dev(c, q, k, v, n_tokens, start_pos, n_heads, n_kv_heads, head_dim,
+                              k_cache, v_cache, cap, s);
+  if (st) return st;
+  st = prefill_attention_locked(c, q, k_cache, v_cache, cap, out, n_tokens, start_pos, n_heads,
+                                n_kv_heads, head_dim, s);
+  return st ? st : set_ok();
 }
 
 // ---------------------------------------------------------------------------

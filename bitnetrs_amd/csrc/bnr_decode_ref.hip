@@ -203,11 +203,11 @@ __device__ __forceinline__ void det_merge(const DecodeArgs &a, int b, int h, int
 // last bits of an output can differ between runs (the two older merges of
 // decode_kernel are deterministic).
 // ---------------------------------------------------------------------------
-// Phase stamps of a measurement build (BNR_DECODE_TIMELINE): wave 0 reads
+// Phase stamps of a measurement build (BNR_TIMELINE): wave 0 reads
 // the 100 MHz real-time counter at the ends of the phases and thread 0
 // stores them when the workgroup ends.  Scheduling barriers keep each read
 // between the instructions of the phases it separates.
-#if defined(BNR_DECODE_TIMELINE)
+#if defined(BNR_TIMELINE)
 #define BNR_STAMP(k)                                   \
   do {                                                 \
     __builtin_amdgcn_sched_barrier(0);                 \
@@ -220,7 +220,7 @@ __device__ __forceinline__ void det_merge(const DecodeArgs &a, int b, int h, int
 
 template <int G, int W, int RPG, bool RAGGED>
 __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
-#if defined(BNR_DECODE_TIMELINE)
+#if defined(BNR_TIMELINE)
   unsigned long long stamp[kTimelineStamps] = {};
   stamp[0] = __builtin_amdgcn_s_memrealtime();
   auto flush_stamps = [&]() {
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(64 * W) void decode_reg_kernel(DecodeArgs a) {
     ref_merge<G>(a, b, h, acc, s_R, s_L, s_mk, tid, 64 * W);
   }
   signal();
-#if defined(BNR_DECODE_TIMELINE)
+#if defined(BNR_TIMELINE)
   __builtin_amdgcn_s_waitcnt(0);  // the output stores have completed
   BNR_STAMP(7);
 #endif
@@ -590,7 +590,7 @@ hipError_t launch_reg_wr(const DecodeArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-#if defined(BNR_DECODE_TIMELINE)
+#if defined(BNR_TIMELINE)
 // Measurement builds only.  One lane runs n dependent device-scope
 // operations (each address depends on the previous result, or an
 // s_waitcnt separates them) and stores the elapsed 100 MHz ticks: the round
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(512) void empty_full_kernel(DecodeArgs a) {
 
 }  // namespace
 
-#if defined(BNR_DECODE_TIMELINE)
+#if defined(BNR_TIMELINE)
 hipError_t launch_rt_probe(unsigned *buf, int n, int mode, unsigned long long *out, hipStream_t s) {
   rt_probe_kernel<<<1, 64, 0, s>>>(buf, n, mode, out);
   return hipGetLastError();

@@ -126,6 +126,36 @@ __device__ __forceinline__ float ld_agent(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The 16- and 8-byte forms of st_agent / ld_agent: buffer stores and loads
+// with the sc1 cache policy (device scope), over a raw buffer that starts at
+// `base`; offsets in bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t agent_buf(const float *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+__device__ __forceinline__ void st4_agent(__amdgpu_buffer_rsrc_t r, int off, float4 v) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v x = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, x),
+                                         r, off, 0, 16);
+}
+__device__ __forceinline__ void st2_agent(__amdgpu_buffer_rsrc_t r, int off, float a, float b) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  const f2v x = {a, b};
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, x),
+                                        r, off, 0, 16);
+}
+__device__ __forceinline__ float4 ld4_agent(__amdgpu_buffer_rsrc_t r, int off) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v v = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float2 ld2_agent(__amdgpu_buffer_rsrc_t r, int off) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  const f2v v = __builtin_bit_cast(f2v, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 16));
+  return make_float2(v.x, v.y);
+}
+
 // Host-slice calls: every thread's stores complete, then thread 0 stores seq
 // into a pinned host word with a system-scope release, so the workgroup's
 // outputs reach the host before the word does.  All threads must call it.

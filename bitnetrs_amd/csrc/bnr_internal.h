@@ -94,7 +94,7 @@ struct DecodeArgs {
   // into done[b * n_kv + h] once that output is visible to the host.
   unsigned *done;
   unsigned seq;
-  // Measurement builds only (compiled with BNR_DECODE_TIMELINE): when
+  // Measurement builds only (compiled with BNR_TIMELINE): when
   // non-null, every workgroup of the reference-merge kernel stores
   // kTimelineStamps s_memrealtime stamps (100 MHz) at
   // timeline[linear block index * kTimelineStamps].  Ignored otherwise.
@@ -219,7 +219,19 @@ struct PrefillArgs {
   // launch's workgroups take equal runs of them.  ws then holds two partial
   // states per workgroup: [2 * workgroups][G][66][64].
   long long sk_units, sk_per_head;
+  // Measurement builds only (compiled with BNR_TIMELINE): when non-null,
+  // workgroup (x, y) of the grid-mapped kernel stores kTimelineStamps words
+  // at timeline[(y * gridDim.x + x) * kTimelineStamps] (PfStamp).  Ignored
+  // otherwise.
+  unsigned long long *timeline;
 };
+// Words of a prefill workgroup's timeline record: 100 MHz s_memrealtime
+// stamps at entry, Q and first K/V tile in LDS, last key tile done, partial
+// state stored and ticket taken (split query tiles; else = key tiles done),
+// merge done (the merging chunk; else 0), output stored (else 0); then the
+// hardware ids (XCC_ID << 32 | HW_ID) and the item (key tiles | nch << 16 |
+// query tile << 32).
+enum PfStamp { kPfEntry, kPfReady, kPfTiles, kPfTicket, kPfMerged, kPfStored, kPfHwId, kPfItem };
 constexpr int kMaxLptChunk = 64;
 constexpr int kPrefillNoSplit = 1 << 20;  // chunk_tiles of an unsplit launch
 constexpr int kPrefillMaxTokens = 32 * 65535;  // query tiles of one tiled prefill launch

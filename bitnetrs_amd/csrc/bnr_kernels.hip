@@ -1,7 +1,8 @@
 // bnr_kernels.hip -- gfx950 decode-side kernels of the GQA attention hot path.
 //
 //  rope_append_kernel  half-split RoPE of q/k + head-major KV append
-//                       (rope_append_vec_kernel: four pairs per thread)
+//                       (rope_append_vec_kernel: four pairs per thread;
+//                       rope_append_row_kernel: one token per workgroup)
 //  decode_kernel<G,RPG> split-K decode attention, head_dim 128, optional
 //                       fused RoPE + append, last-workgroup merge
 //  decode_merge_kernel  second kernel of the two-launch merge
@@ -100,6 +101,56 @@ __global__ __launch_bounds__(256) void rope_append_vec_kernel(RopeAppendArgs a) 
     }
   }
   if (a.done) signal_host(a.done + blockIdx.x, a.seq);
+}
+
+// One token per workgroup, head_dim 128 (device calls; no host signal):
+// thread t rotates quad t % 16 of heads t / 16, t / 16 + 16, ... (the q
+// heads, then the k heads) with one load of its table quad, and copies the
+// token's v rows a float4 at a time.  The same rotation as
+// rope_append_kernel, element for element.  All of a thread's loads are
+// issued before its first store (a store to q or k could otherwise alias
+// the next load for the compiler).
+__global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) {
+  constexpr int half = kHeadDim / 2;
+  const int tok = blockIdx.x, pos = a.start_pos + tok;
+  const int t = threadIdx.x, i = 4 * (t & 15);
+  const int nrot = a.n_heads + a.n_kv;
+  auto row = [&](int h) {
+    return h < a.n_heads ? a.q + ((long long)tok * a.n_heads + h) * kHeadDim
+                         : a.k + ((long long)tok * a.n_kv + (h - a.n_heads)) * kHeadDim;
+  };
+  auto finish = [&](int h, float *x, float4 lo, float4 hi) {
+    st4(x + i, lo);
+    st4(x + i + half, hi);
+    if (h >= a.n_heads && a.k_cache) {
+      float *dst = a.k_cache + (h - a.n_heads) * a.kv_stride + (long long)pos * kHeadDim;
+      st4(dst + i, lo);
+      st4(dst + i + half, hi);
+    }
+  };
+  const float4 c = ld4(a.cos_tab + (long long)pos * half + i);
+  const float4 sn = ld4(a.sin_tab + (long long)pos * half + i);
+  for (int h = t >> 4; h < nrot; h += 32) {
+    // heads h and h + 16: both rows loaded, then both rotated and stored
+    const int h2 = h + 16;
+    float *x1 = row(h), *x2 = h2 < nrot ? row(h2) : x1;
+    const float4 a_lo = ld4(x1 + i), a_hi = ld4(x1 + i + half);
+    const float4 b_lo = ld4(x2 + i), b_hi = ld4(x2 + i + half);
+    float4 lo, hi;
+    rot4(a_lo, a_hi, c, sn, lo, hi);
+    float4 lo2, hi2;
+    rot4(b_lo, b_hi, c, sn, lo2, hi2);
+    finish(h, x1, lo, hi);
+    if (h2 < nrot) finish(h2, x2, lo2, hi2);
+  }
+  if (a.v_cache) {
+    constexpr int F = kHeadDim / 4;  // float4 per row
+    for (int f = t; f < a.n_kv * F; f += 256) {
+      const int hv = f / F, j = 4 * (f % F);
+      const float4 v = ld4(a.v + ((long long)tok * a.n_kv + hv) * kHeadDim + j);
+      st4(a.v_cache + hv * a.kv_stride + (long long)pos * kHeadDim + j, v);
+    }
+  }
 }
 
 // Merge the nsplit partial states of (sequence b, kv head h) into the
@@ -758,6 +809,10 @@ long long rope_append_blocks(const RopeAppendArgs &a) {
 
 hipError_t launch_rope_append(const RopeAppendArgs &a, hipStream_t s) {
   const bool vec = rope_append_vec(a);
+  if (vec && !a.done && a.head_dim == kHeadDim && a.n_tokens > 0) {
+    rope_append_row_kernel<<<dim3((unsigned)a.n_tokens), dim3(256), 0, s>>>(a);
+    return hipGetLastError();
+  }
   const long long blocks = rope_append_blocks(a);
   if (blocks == 0) return hipSuccess;
   if (vec)

@@ -57,6 +57,22 @@ __device__ __forceinline__ void dma16(const float *g, float *lds) {
 // s_waitcnt vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Timeline stamps of a measurement build (BNR_TIMELINE): every wave reads
+// the 100 MHz real-time counter into its copy of the record (PfStamp) and
+// thread 0 stores wave 0's copy when the workgroup ends.  Scheduling
+// barriers keep each read between the instructions of the phases it
+// separates.  Product builds compile the stamps away.
+#if defined(BNR_TIMELINE)
+#define PF_STAMP(st, k)                                                  \
+  do {                                                                   \
+    __builtin_amdgcn_sched_barrier(0);                                   \
+    if (st) (st)[k] = __builtin_amdgcn_s_memrealtime();                  \
+    __builtin_amdgcn_sched_barrier(0);                                   \
+  } while (0)
+#else
+#define PF_STAMP(st, k) ((void)0)
+#endif
+
 // Two waves per SIMD: at most 256 registers per lane.  (G = 2 reaches only
 // one: two of its workgroups fill LDS.)
 #pragma clang diagnostic push
@@ -110,6 +126,26 @@ __device__ __forceinline__ void pf_copy_part(const PrefillArgs &a, int h, int kt
   const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
   dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
   dma16(vc + grow + 4 * p, dv + J * 256);
+}
+// The K half (dv null) or the V half (dk null) of a tile's copies.
+template <int G>
+__device__ __forceinline__ void pf_copy_half(const PrefillArgs &a, int h, int kt, float *dk,
+                                             float *dv) {
+  constexpr int NI = kPrefillTile / 4 / (64 * G);
+  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int last_row = a.start_pos + a.n_tokens - 1;
+  const float *src = (dk ? a.k_cache : a.v_cache) + h * a.kv_stride;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int J = wave * NI + j;
+    const int r = 2 * J + hl, p = col;
+    const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
+    if (dk)
+      dma16(src + grow + 4 * (p ^ (r & 15)), dk + J * 256);
+    else
+      dma16(src + grow + 4 * p, dv + J * 256);
+  }
 }
 template <int G>
 __device__ __forceinline__ void pf_copy_tile(const PrefillArgs &a, int h, int kt, float *dk,
@@ -251,20 +287,24 @@ __device__ __forceinline__ void pf_tile_pv(const PrefillArgs &a, const PfItem &i
 // registers and, like an unsplit item, writes the output.
 template <int G>
 __device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it,
-                                          floatx16 (&O)[4], float m, float l, int *s_last) {
+                                          floatx16 (&O)[4], float m, float l, int *s_last,
+                                          unsigned long long *stamp = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, col = lane & 31;
   const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = it.h, head = h * G + g;
   if (it.nch > 1) {
-    // Partial state of this chunk, lane-coalesced: component c (0..63 O, 64 m,
-    // 65 l) of lane `lane` of wave g at ws[((item * G + g) * 66 + c) * 64 + lane].
-    float *slot = a.ws + (((long long)h * a.n_items + it.base + it.ch) * G + g) * 66 * 64 + lane;
+    // Partial state of this chunk, 16 bytes per lane and instruction: the
+    // float4 k (components 4k .. 4k+3 of O, component c = 16*db + r) of lane
+    // `lane` of wave g at float ((k * 64 + lane) * 4) of the slot, then m
+    // and l of the lane as a pair at float 64 * 64 + 2 * lane.
+    const long long slot = (((long long)h * a.n_items + it.base + it.ch) * G + g) * 66 * 64;
+    const __amdgpu_buffer_rsrc_t mine = agent_buf(a.ws + slot);
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) st_agent(slot + (16 * db + r) * 64, O[db][r]);
-    st_agent(slot + 64 * 64, m);
-    st_agent(slot + 65 * 64, l);
+    for (int k = 0; k < 16; ++k)
+      st4_agent(mine, (k * 64 + lane) * 16,
+                make_float4(O[k >> 2][4 * (k & 3)], O[k >> 2][4 * (k & 3) + 1],
+                            O[k >> 2][4 * (k & 3) + 2], O[k >> 2][4 * (k & 3) + 3]));
+    st2_agent(mine, 64 * 64 * 4 + 8 * lane, m, l);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
     __syncthreads();
     unsigned *ctr = a.counters + ((long long)h * a.n_qtiles + it.qt) * kCounterStride;
@@ -276,25 +316,33 @@ __device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it
     __syncthreads();
     const bool last = *s_last;
     __syncthreads();  // s_last is read before the next item may write it
+    PF_STAMP(stamp, kPfTicket);
     if (!last) return;
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Merge the other chunks into this one's registers (same lane layout).
     for (int c = 0; c < it.nch; ++c) {
       if (c == it.ch) continue;
-      const float *src = a.ws + (((long long)h * a.n_items + it.base + c) * G + g) * 66 * 64 + lane;
-      float ov[64];
+      const __amdgpu_buffer_rsrc_t src = agent_buf(
+          a.ws + (((long long)h * a.n_items + it.base + c) * G + g) * 66 * 64);
+      float4 ov[16];
 #pragma unroll
-      for (int i = 0; i < 64; ++i) ov[i] = ld_agent(src + i * 64);
-      const float mc = ld_agent(src + 64 * 64), lc = ld_agent(src + 65 * 64);
-      const float mn = fmaxf(m, mc);
-      const float sa = fast_exp2(m - mn), sb = fast_exp2(mc - mn);
-      l = l * sa + lc * sb;
+      for (int k = 0; k < 16; ++k) ov[k] = ld4_agent(src, (k * 64 + lane) * 16);
+      const float2 ml = ld2_agent(src, 64 * 64 * 4 + 8 * lane);
+      const float mn = fmaxf(m, ml.x);
+      const float sa = fast_exp2(m - mn), sb = fast_exp2(ml.x - mn);
+      l = l * sa + ml.y * sb;
       m = mn;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) O[db][r] = O[db][r] * sa + ov[16 * db + r] * sb;
+      for (int k = 0; k < 16; ++k) {
+        floatx16 &o = O[k >> 2];
+        const int r = 4 * (k & 3);
+        o[r] = o[r] * sa + ov[k].x * sb;
+        o[r + 1] = o[r + 1] * sa + ov[k].y * sb;
+        o[r + 2] = o[r + 2] * sa + ov[k].z * sb;
+        o[r + 3] = o[r + 3] * sa + ov[k].w * sb;
+      }
     }
+    PF_STAMP(stamp, kPfMerged);
   }
   // Lane (col, hl) holds, for r = 4*rq + r3, dims 32*rq + 16*hl + 4*r3 + db.
   const float inv = 1.0f / (l + __shfl_xor(l, 32));
@@ -305,6 +353,7 @@ __device__ __forceinline__ void pf_finish(const PrefillArgs &a, const PfItem &it
       st4(op + 32 * (r >> 2) + 4 * (r & 3),
           make_float4(O[0][r] * inv, O[1][r] * inv, O[2][r] * inv, O[3][r] * inv));
   }
+  PF_STAMP(stamp, kPfStored);
 }
 
 // Grid-mapped prefill: workgroup (h = blockIdx.x, y = blockIdx.y), kv head
@@ -319,35 +368,71 @@ void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) float sV0[kPrefillTile];
   __shared__ __attribute__((aligned(16))) float sV1[kPrefillTile];
   __shared__ int s_last;
+#if defined(BNR_TIMELINE)
+  unsigned long long stamp_buf[kTimelineStamps] = {};
+  unsigned long long *stamp = stamp_buf;
+  PF_STAMP(stamp, kPfEntry);
+#else
+  unsigned long long *stamp = nullptr;
+#endif
   const PfItem it = pf_item(a, blockIdx.x, blockIdx.y);
-  pf_copy_tile<G>(a, it.h, it.kt0, sK0, sV0);
+  // Start: the first tile's K and the Q fragment are waited for; its V
+  // lands under the first tile's K products.
+  constexpr int NI = kPrefillTile / 4 / (64 * G);  // copies per wave per half tile
+  pf_copy_half<G>(a, it.h, it.kt0, sK0, nullptr);
   float qf[64];
   pf_load_q<G>(a, it, qf);
+  pf_copy_half<G>(a, it.h, it.kt0, nullptr, sV0);
   pf_scale_q(qf, a.scale_log2);
-  wait_vmem();
-  __syncthreads();
+  // All but this wave's NI V copies, then a bare barrier: a fenced one
+  // (__syncthreads) would wait for every copy in flight.
+  __builtin_amdgcn_s_waitcnt(0x0F70 | NI);
+  __builtin_amdgcn_s_barrier();
+  PF_STAMP(stamp, kPfReady);
   floatx16 O[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) O[db] = floatx16{};
   // m starts finite: in a chunk that is not the first, a query may see no key
   // at all (p = 0 for it throughout, and no -inf - -inf in the rescale).
   float m = -1e30f, l = 0.f;
-  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv) {
+  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv, bool first) {
     // The next tile's copies go out between this tile's K products (the
     // last tile copies itself again into the free buffers, so that the copy
     // needs no branch and shares the products' block).
     const floatx16 S = pf_tile_s_copy<G>(dk, qf, a, it.h, min(kt + 1, it.nkt - 1), nk, nv);
+    if (first) {
+      // the first tile's V: every wave's copies landed (only the next
+      // tile's 2 NI copies of this wave may still be in flight)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NI));
+      __builtin_amdgcn_s_barrier();
+    }
     pf_tile_pv(a, it, kt, S, dv, O, m, l);
     wait_vmem();  // this wave's copies of the next tile have landed
     __syncthreads();
   };
-  for (int kt = it.kt0;;) {
-    step(kt, sK0, sV0, sK1, sV1);
+  step(it.kt0, sK0, sV0, sK1, sV1, true);
+  for (int kt = it.kt0 + 1; kt < it.nkt;) {
+    step(kt, sK1, sV1, sK0, sV0, false);
     if (++kt >= it.nkt) break;
-    step(kt, sK1, sV1, sK0, sV0);
-    if (++kt >= it.nkt) break;
+    step(kt, sK0, sV0, sK1, sV1, false);
+    ++kt;
   }
-  pf_finish<G>(a, it, O, m, l, &s_last);
+  PF_STAMP(stamp, kPfTiles);
+  pf_finish<G>(a, it, O, m, l, &s_last, stamp);
+#if defined(BNR_TIMELINE)
+  if (a.timeline && threadIdx.x == 0) {
+    if (it.nch == 1) stamp_buf[kPfTicket] = stamp_buf[kPfTiles];
+    constexpr int kHwId = 4 | (31 << 11), kXccId = 20 | (15 << 11);  // HW_REG_HW_ID, HW_REG_XCC_ID
+    stamp_buf[kPfHwId] = ((unsigned long long)(unsigned)__builtin_amdgcn_s_getreg(kXccId) << 32) |
+                         (unsigned)__builtin_amdgcn_s_getreg(kHwId);
+    stamp_buf[kPfItem] = (unsigned long long)(it.nkt - it.kt0) | ((unsigned long long)it.nch << 16) |
+                         ((unsigned long long)it.qt << 32);
+    unsigned long long *rec =
+        a.timeline + ((long long)blockIdx.y * gridDim.x + blockIdx.x) * kTimelineStamps;
+#pragma unroll
+    for (int k = 0; k < kTimelineStamps; ++k) rec[k] = stamp_buf[k];
+  }
+#endif
 }
 
 // Persistent prefill: gridDim.x resident workgroups (at most the number of

@@ -469,8 +469,12 @@ def test_dev_prefill_shapes(backend, n_heads, n_kv, n_tokens, start):
     q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
                                                   n_heads=n_heads, n_kv=n_kv)
     out = torch.zeros(n_tokens, n_heads * D, device="cuda")
-    backend.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads, n_kv, D,
+    q_d, k_d = dev(w["q"]), dev(w["k"])
+    backend.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads, n_kv, D,
                         THETA, d_kc, d_vc, cap, out)
+    # q and k rotated in place, bit for bit
+    np.testing.assert_array_equal(host(q_d), q_ref)
+    np.testing.assert_array_equal(host(k_d), k_ref)
     np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
     assert_close(host(out), out_ref, f"prefill {n_heads}/{n_kv} n {n_tokens}")
 
@@ -504,10 +508,15 @@ def test_dev_prefill_key_chunks(monkeypatch, tiles, persistent):
         start = 45
         for n_tokens, s in ((300, 37), (129, 38)):
             w = prefill_workload(s, n_tokens)
-            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be)
             out = torch.zeros(n_tokens, HQ * D, device="cuda")
-            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, HQ, HKV, D,
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, HQ, HKV, D,
                                THETA, d_kc, d_vc, cap, out)
+            # q and k rotated in place, bit for bit
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
             assert_close(host(out), out_ref, f"prefill chunks of {tiles} n {n_tokens} start {start}")
             start += n_tokens
     finally:
@@ -541,11 +550,15 @@ def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persis
         start = 45
         for n_tokens, s in ((230, 41), (200, 42)):
             w = prefill_workload(s, n_tokens, n_heads, n_kv)
-            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
-                                                  n_heads=n_heads, n_kv=n_kv)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be, n_heads=n_heads, n_kv=n_kv)
             out = torch.zeros(n_tokens, n_heads * D, device="cuda")
-            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads,
                                n_kv, D, THETA, d_kc, d_vc, cap, out)
+            # q and k rotated in place, bit for bit
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
             np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
             assert_close(host(out), out_ref,
                          f"prefill {n_heads}/{n_kv} chunks of {tiles} n {n_tokens} start {start}")
@@ -586,11 +599,15 @@ def test_dev_prefill_balanced_chunks(monkeypatch, n_heads, n_kv, tiles, persiste
         start = 45
         for n_tokens, s in ((300, 47), (129, 48)):
             w = prefill_workload(s, n_tokens, n_heads, n_kv)
-            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
-                                                  n_heads=n_heads, n_kv=n_kv)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be, n_heads=n_heads, n_kv=n_kv)
             out = torch.zeros(n_tokens, n_heads * D, device="cuda")
-            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads,
                                n_kv, D, THETA, d_kc, d_vc, cap, out)
+            # q and k rotated in place, bit for bit
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
             np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
             assert_close(host(out), out_ref,
                          f"prefill balanced {n_heads}/{n_kv} chunks of {tiles} n {n_tokens} "
@@ -630,11 +647,15 @@ def test_dev_prefill_streamk(monkeypatch, n_heads, n_kv, wgs):
         start = 45
         for n_tokens, s in ((333, 45), (1, 46), (300, 47)):
             w = prefill_workload(s, n_tokens, n_heads, n_kv)
-            _, _, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache, backend=be,
-                                                  n_heads=n_heads, n_kv=n_kv)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be, n_heads=n_heads, n_kv=n_kv)
             out = torch.zeros(n_tokens, n_heads * D, device="cuda")
-            be_gpu.dev_prefill(dev(w["q"]), dev(w["k"]), dev(w["v"]), n_tokens, start, n_heads,
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads,
                                n_kv, D, THETA, d_kc, d_vc, cap, out)
+            # q and k rotated in place, bit for bit
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
             np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
             assert_close_scaled(host(out), out_ref,
                                 f"stream-K {n_heads}/{n_kv} wgs {wgs} n {n_tokens} start {start}")
