@@ -900,7 +900,9 @@ def decode_timeline_main(args) -> int:
     medians over launches (us): the phases of the workgroup that finishes
     last (the critical path), the same phases over all workgroups, the
     dispatch spread, and the gap from one launch's last stamp to the next
-    launch's first."""
+    launch's first.  With --batched-timeline: the same for the 32-sequence
+    batched decode (one launch per step; splits past a sequence's end are
+    left out)."""
     import ctypes
 
     import numpy as np
@@ -920,22 +922,40 @@ def decode_timeline_main(args) -> int:
     lib.bnr_debug_decode_timeline.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     be = bitnetrs_amd.HipBackend(0)
     log(f"device: {be.device_name()} (timeline build)")
-    n_layers, L, pos, cap = 32, 4096, 4095, 4096
     steps, reps = args.steps, args.replays
-    g = torch.Generator(device="cuda").manual_seed(0xB17E7020)
-    kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
-    vc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
-    q = torch.randn(n_layers, HQ * D, device="cuda", generator=g) * 4.0
-    k = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
-    v = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
-    out = torch.zeros(n_layers, HQ * D, device="cuda")
-    max_wg = 256 * HKV  # at most 256 splits per kv head
+    batched = args.batched_timeline
+    if batched:
+        # the batched workload: 32 sequences, lengths ~ U[128, 4096), one launch a step
+        n_seq, cap = 32, 4096
+        lens = np.random.default_rng(0xB17E7040).integers(128, 4096, size=n_seq).astype(np.int32)
+        g = torch.Generator(device="cuda").manual_seed(0xB17E7041)
+        kc = torch.randn(n_seq, HKV, cap, D, device="cuda", generator=g)
+        vc = torch.randn(n_seq, HKV, cap, D, device="cuda", generator=g)
+        q = torch.randn(n_seq, HQ * D, device="cuda", generator=g)
+        k = torch.randn(n_seq, HKV * D, device="cuda", generator=g)
+        v = torch.randn(n_seq, HKV * D, device="cuda", generator=g)
+        out = torch.zeros(n_seq, HQ * D, device="cuda")
+        max_wg = 256 * HKV * n_seq
+    else:
+        n_layers, pos, cap = 32, 4095, 4096
+        g = torch.Generator(device="cuda").manual_seed(0xB17E7020)
+        kc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+        vc = torch.randn(n_layers, HKV, cap, D, device="cuda", generator=g)
+        q = torch.randn(n_layers, HQ * D, device="cuda", generator=g) * 4.0
+        k = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+        v = torch.randn(n_layers, HKV * D, device="cuda", generator=g)
+        out = torch.zeros(n_layers, HQ * D, device="cuda")
+        max_wg = 256 * HKV  # at most 256 splits per kv head
     stamps = torch.zeros(steps, max_wg * 8, dtype=torch.int64, device="cuda")
 
     def step(i, rec=True):
-        r = i % n_layers
         _lib.check(lib.bnr_debug_decode_timeline(be._h, stamps[i].data_ptr() if rec else None))
-        be.dev_decode_step(q[r], k[r], v[r], pos, HQ, HKV, D, THETA, kc[r], vc[r], cap, out[r])
+        if batched:
+            be.dev_decode_step_batched(q, k, v, lens, HQ, HKV, D, THETA, kc, vc, cap, out)
+        else:
+            r = i % n_layers
+            be.dev_decode_step(q[r], k[r], v[r], pos, HQ, HKV, D, THETA, kc[r], vc[r], cap,
+                               out[r])
 
     for i in range(args.warmup):
         step(i, rec=False)
@@ -961,6 +981,7 @@ def decode_timeline_main(args) -> int:
         for i in range(steps):
             rows = st[i][st[i][:, 0] != 0]
             t_first = rows[:, 0].min()
+            rows = rows[rows[:, 2] != 0]  # ragged launches: splits past a sequence's end exit
             end = rows[:, 1:].max()
             firsts.append(t_first)
             lasts.append(end)
@@ -991,7 +1012,9 @@ def decode_timeline_main(args) -> int:
     # the first launch's dispatch and the last one's end)
     tick_us = 1.0 / 100.0
     med = lambda xs: float(np.median(xs))  # noqa: E731
-    res = {"workload": "gqa_decode_step_L4096_hq20_hkv5_d128_fp32 (timeline build)",
+    res = {"workload": ("gqa_decode_step_batch32_ragged_len_U128_4096_hq20_hkv5_d128_fp32"
+                        if batched else "gqa_decode_step_L4096_hq20_hkv5_d128_fp32")
+                       + " (timeline build)",
            "launches": len(samples), "steps": steps, "replays": reps,
            "wgs_per_launch": int(samples[0]["wgs"]),
            "graph_step_us": round(med(per_step) * 1e3, 3),
@@ -1025,7 +1048,7 @@ def decode_timeline_main(args) -> int:
                                  "atomic_add", "system_store", "decode_footprint"]):
         # on the capturing stream (a NULL stream would not be captured)
         empty = capture(torch, lambda i: _lib.check(lib.bnr_debug_empty_launch(
-            be._h, wgs, 512, mode, wbuf.data_ptr(),
+            be._h, wgs, 256 if batched else 512, mode, wbuf.data_ptr(),
             ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))), steps)
         res[f"empty_launch_{name}_graph_step_us"] = round(
             replay_stats(torch, empty, steps, reps=reps)["median"] * 1e3, 3)
@@ -1224,6 +1247,8 @@ def main() -> int:
     ap.add_argument("--decode-timeline", action="store_true",
                     help="only the per-phase timeline of the decode kernel (loads the "
                          "measurement build libbitnet_hip_timeline.so)")
+    ap.add_argument("--batched-timeline", action="store_true",
+                    help="with --decode-timeline: the 32-sequence batched decode instead")
     ap.add_argument("--prefill-timeline", action="store_true",
                     help="only the per-workgroup timeline of the stack-shape prefill (loads the "
                          "measurement build libbitnet_hip_timeline.so; --prefill-tokens sets N)")

@@ -109,7 +109,9 @@ __global__ __launch_bounds__(256) void rope_append_vec_kernel(RopeAppendArgs a) 
 // token's v rows a float4 at a time.  The same rotation as
 // rope_append_kernel, element for element.  All of a thread's loads are
 // issued before its first store (a store to q or k could otherwise alias
-// the next load for the compiler).
+// the next load for the compiler).  The raw rows are read once:
+// non-temporal loads (1024 tokens x 20/5 heads: 9.9 -> 8.2 us per graph
+// step on MI355X).
 __global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) {
   constexpr int half = kHeadDim / 2;
   const int tok = blockIdx.x, pos = a.start_pos + tok;
@@ -134,8 +136,8 @@ __global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) 
     // heads h and h + 16: both rows loaded, then both rotated and stored
     const int h2 = h + 16;
     float *x1 = row(h), *x2 = h2 < nrot ? row(h2) : x1;
-    const float4 a_lo = ld4(x1 + i), a_hi = ld4(x1 + i + half);
-    const float4 b_lo = ld4(x2 + i), b_hi = ld4(x2 + i + half);
+    const float4 a_lo = ld4_nt(x1 + i), a_hi = ld4_nt(x1 + i + half);
+    const float4 b_lo = ld4_nt(x2 + i), b_hi = ld4_nt(x2 + i + half);
     float4 lo, hi;
     rot4(a_lo, a_hi, c, sn, lo, hi);
     float4 lo2, hi2;
@@ -147,7 +149,7 @@ __global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) 
     constexpr int F = kHeadDim / 4;  // float4 per row
     for (int f = t; f < a.n_kv * F; f += 256) {
       const int hv = f / F, j = 4 * (f % F);
-      const float4 v = ld4(a.v + ((long long)tok * a.n_kv + hv) * kHeadDim + j);
+      const float4 v = ld4_nt(a.v + ((long long)tok * a.n_kv + hv) * kHeadDim + j);
       st4(a.v_cache + hv * a.kv_stride + (long long)pos * kHeadDim + j, v);
     }
   }
