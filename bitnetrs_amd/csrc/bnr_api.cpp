@@ -163,8 +163,9 @@ void fingerprint(const uint8_t *p, size_t len, uint8_t *out) {
 constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
-  int n_tokens, start_pos, n_kv, tiles, balanced;
+  int n_tokens, start_pos, n_kv;
   long long cap;
+  PrefillChoice choice;
 };
 
 struct DeviceGuard {
@@ -274,6 +275,7 @@ struct bnr_ctx {
   int pf_chunk_tiles = -1;  // -1: planner decides; else key tiles per chunk
   int pf_mode = kPrefillAuto;  // tiled prefill launch: kPrefillAuto / Grid / Queue / StreamK
   int pf_sk_wgs = 0;              // stream-K workgroups (0: every resident slot)
+  int pf_q16 = -1;                // 16-query halves (prefill16_kernel): -1 planner, 0 never, 1 always
   int pf_balanced = -1;           // balanced key chunks: -1 planner, 0 never, 1 always
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
@@ -498,22 +500,18 @@ void free_ws(DecodeWs &w) {
 // the library's own stream, the device entry points on the caller's.
 DecodeWs &ws_for(bnr_ctx *c, hipStream_t s) { return s == c->stream ? c->hws : c->dws; }
 
-// The planner's chunk size for a prefill shape, remembered for the last 16
+// The planner's choice for a prefill shape, remembered for the last 16
 // shapes (planning replays the dispatch for every candidate).
-int plan_prefill_cached(bnr_ctx *c, int n_tokens, int start_pos, int n_kv, long long cap,
-                        int *balanced) {
+PrefillChoice plan_prefill_cached(bnr_ctx *c, int n_tokens, int start_pos, int n_kv,
+                                  long long cap) {
   for (const PrefillPlanEntry &e : c->pf_plans)
-    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv && e.cap == cap) {
-      *balanced = e.balanced;
-      return e.tiles;
-    }
-  int bal = 0;
-  const int tiles =
-      plan_prefill_chunk(n_tokens, start_pos, n_kv, c->n_cu, c->pf_balanced, cap, &bal);
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv && e.cap == cap)
+      return e.choice;
+  const PrefillChoice ch =
+      plan_prefill_chunk(n_tokens, start_pos, n_kv, c->n_cu, c->pf_balanced, c->pf_q16, cap);
   if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
-  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, tiles, bal, cap});
-  *balanced = bal;
-  return tiles;
+  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, cap, ch});
+  return ch;
 }
 
 // RopeCache::new (bitnet-cpu/src/rope.rs:100-153) on the host: same f32
@@ -896,6 +894,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (const char *v = std::getenv("BNR_PREFILL_PERSISTENT"))
     if (atoi(v) > 0) c->pf_mode = kPrefillQueue;
   if (const char *v = std::getenv("BNR_PREFILL_SK_WGS")) c->pf_sk_wgs = std::max(atoi(v), 0);
+  if (const char *v = std::getenv("BNR_PREFILL_Q16")) c->pf_q16 = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_BALANCED")) c->pf_balanced = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_MODE")) {
     const int m = atoi(v);
@@ -1671,13 +1670,17 @@ bool prefill_tiled(size_t n_tokens, size_t start_pos, size_t n_heads, size_t n_k
 }
 
 // Stream-K where every query tile has about as many keys as the next (a
-// cached prefix at least as long as the new tokens: 512 queries after 1536
-// cached rows 98 vs 100 us, 1024 after 3000 303 vs 312 us on MI355X);
-// planned key chunks otherwise (N = 1024 from an empty cache: 73 vs 85 us,
-// N = 4096: 676 vs 710 us).
+// cached prefix at least as long as the new tokens) and the tokens are more
+// than 512: 1024 after 3000 305 us against 316 us for the planned 16-query
+// chunks and 312 us for 32-query ones, 1024 after 1024 155 us against 147-
+// 154 us (MI355X, graph-timed).  Planned chunks otherwise -- from an empty
+// cache (N = 1024: 62 vs 85 us, N = 4096: 671 vs 710 us) and for short
+// launches after a long prefix, where the 16-query kernel wins (512 after
+// 512: 48 vs 61 us, 256 after 1024: 38 vs 56 us).
 bool prefill_streamk(const bnr_ctx *c, size_t n_tokens, size_t start_pos) {
   return c->pf_chunk_tiles <= 0 &&
-         (c->pf_mode == kPrefillStreamK || (c->pf_mode == kPrefillAuto && start_pos >= n_tokens));
+         (c->pf_mode == kPrefillStreamK ||
+          (c->pf_mode == kPrefillAuto && start_pos >= n_tokens && n_tokens > 512));
 }
 
 // Prefill attention with c->mu held.
@@ -1706,12 +1709,17 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
     const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
     const bool streamk = prefill_streamk(c, n_tokens, start_pos);
     if (!streamk) {
-      int bal = c->pf_balanced == 1;
-      pa.chunk_tiles = c->pf_chunk_tiles > 0
-                           ? c->pf_chunk_tiles
-                           : plan_prefill_cached(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads,
-                                                 (long long)cap, &bal);
-      pa.balanced = bal;
+      if (c->pf_chunk_tiles > 0) {
+        pa.chunk_tiles = c->pf_chunk_tiles;
+        pa.balanced = c->pf_balanced == 1;
+        pa.q16 = c->pf_q16 == 1;
+      } else {
+        const PrefillChoice ch = plan_prefill_cached(c, (int)n_tokens, (int)start_pos,
+                                                     (int)n_kv_heads, (long long)cap);
+        pa.chunk_tiles = ch.tiles;
+        pa.balanced = ch.balanced;
+        pa.q16 = ch.q16;
+      }
     } else {
       pa.chunk_tiles = kPrefillNoSplit;
     }
@@ -1736,8 +1744,10 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
       st = ensure_buf(&c->pf_ws, &c->pf_ws_floats, (size_t)items * group * 66 * 64,
                       "prefill workspace alloc");
       if (st) return st;
+      // tickets: one per (kv head, query tile, 16-query half)
       st = ensure_zeroed(&c->pf_counters, &c->n_pf_counters,
-                         (size_t)n_kv_heads * std::max<long long>(T, pa.n_qtiles) * kCounterStride);
+                         (size_t)n_kv_heads * std::max<long long>(T, pa.n_qtiles) * 2 *
+                             kCounterStride);
       if (st) return st;
     }
     if (streamk) {
@@ -1756,6 +1766,7 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
       pa.counters = c->pf_counters;
     }
     int pwgs = 0;
+    if (c->pf_mode == kPrefillQueue) pa.q16 = 0;  // the persistent kernel runs whole tiles
     if (c->pf_mode == kPrefillQueue) {
       st = ensure_zeroed(&c->pf_queue, &c->n_pf_queue, 2 * kCounterStride);
       if (st) return st;

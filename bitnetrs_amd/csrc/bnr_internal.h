@@ -214,6 +214,10 @@ struct PrefillArgs {
   // key tiles (prefill_order fills it).
   int balanced;
   int bal_off[65];
+  // Grid-mapped launches: q16 = 1 runs every item as two 16-query halves
+  // (prefill16_kernel; grid x = 2 n_kv); counters then hold one ticket per
+  // (kv head, query tile, half).
+  int q16;
   // Stream-K launch (sk_units > 0): units = (kv head, query tile, key tile)
   // tile products in that order, sk_per_head of them per kv head; the
   // launch's workgroups take equal runs of them.  ws then holds two partial
@@ -421,9 +425,20 @@ void prefill_order(PrefillArgs &a);
 // launch at ctiles key tiles per chunk.  plan_prefill_chunk: the planner's
 // key tiles per chunk (kPrefillNoSplit: none) and *balanced for one shape,
 // among the candidates that fit prefill_item_budget(cap, n_kv).
-double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles, int n_cu, bool balanced);
-int plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
-                       long long cap, int *balanced);
+double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles, int n_cu, bool balanced,
+                    bool q16 = false);
+// The planner's choice for one launch shape: key tiles per chunk
+// (kPrefillNoSplit: none), balanced chunks, 16-query halves.
+struct PrefillChoice {
+  int tiles, balanced, q16;
+};
+// bal_pref / q16_pref: -1 either, 0 never, 1 always.
+PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
+                                 int q16_pref, long long cap);
+// Constants of the 16-query halves in the span model (fixed cost, key tile,
+// merge per extra chunk; a 32-query tile alone on a CU takes 1) and the
+// span ratio below which the planner switches to them.
+extern double g_pf16_fixed, g_pf16_tile, g_pf16_merge, g_pf16_margin;
 long long prefill_item_budget(long long cap, int n_kv);
 constexpr long long kPrefillMaxPlannedItems = 8192;
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.

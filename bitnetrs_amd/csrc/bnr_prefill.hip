@@ -435,6 +435,296 @@ void prefill_kernel(PrefillArgs a) {
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// 16-query prefill (v_mfma_f32_16x16x4_f32).  The items, key chunks,
+// partial-state slots and merge of the grid-mapped launch, each item run by
+// two workgroups: half 0 takes queries q0 .. q0+15 of the item's 32-query
+// tile, half 1 q0+16 .. q0+31 (grid x = 2 n_kv, x = 2 h + half).  A
+// workgroup is G waves (one per q head of kv head h) x 16 queries sharing
+// prefill_kernel's double-buffered K/V tiles; a tile product is half as long
+// and needs half the Q fragment.
+//
+// Lane l: query j = l % 16 of the half, lane group u = l / 16.  S^T (32 keys
+// x 16 queries) is two 16x16 blocks b; MFMA step t multiplies K (A: lane l
+// holds key 16b + j) by Q^T (B: lane l holds query j) at head dim
+// 16 (t/4) + 4u + t%4, so a lane reads one 16-byte chunk of its K row per
+// four steps and holds its Q dims as 8 float4s.  Register r of S^T block b
+// holds key 16b + 4u + r of query j: exactly the B operand P^T of PV step
+// 4b + r, whose A operand V^T takes, for O^T block n (0..7), head dim
+// 64 (n/4) + 4 j + n%4 of key row 16b + 4u + r -- two float4 reads of the
+// row (dims 4j.. and 64+4j..) feed the eight blocks, and the 16 lanes of a
+// lane group read 256 contiguous bytes.  O^T register r of block n holds
+// dim 64 (n/4) + 16u + 4r + n%4 of query j.  A query's tile maximum and sum
+// span the lanes j, j+16, j+32, j+48 (two lane swaps).
+// ---------------------------------------------------------------------------
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// max(v) and sum(v) over the lanes l, l^16, l^32, l^48: one
+// v_permlane16_swap and one v_permlane32_swap; either copy of a swapped
+// pair holds the other row's value, so max / sum of the pair is the pair's.
+__device__ __forceinline__ float quad_max(float v) {
+  unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+  u = __builtin_bit_cast(unsigned, v);
+  const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)s[0]), __builtin_bit_cast(float, (unsigned)s[1]));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+  unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  u = __builtin_bit_cast(unsigned, v);
+  const auto s = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)s[0]) + __builtin_bit_cast(float, (unsigned)s[1]);
+}
+
+// This lane's Q fragment: dims 16m + 4u + e of query q0h + j, unscaled.
+template <int G>
+__device__ __forceinline__ void pf16_load_q(const PrefillArgs &a, int h, int q0h, float (&qf)[32]) {
+  const int lane = threadIdx.x & 63, j = lane & 15, u = lane >> 4;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qrow = min(q0h + j, a.n_tokens - 1);  // rows past the end are not stored
+  const float *qp = a.q + ((long long)qrow * a.n_heads + h * G + g) * kHeadDim + 4 * u;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float4 v = ld4(qp + 16 * m);
+    qf[4 * m] = v.x;
+    qf[4 * m + 1] = v.y;
+    qf[4 * m + 2] = v.z;
+    qf[4 * m + 3] = v.w;
+  }
+}
+
+// S^T of one key tile (blocks 0 and 1) with the next tile's copies issued
+// between the products (as pf_tile_s_copy) and each K chunk read one group
+// ahead of its use.
+template <int G>
+__device__ __forceinline__ void pf16_tile_s_copy(const float *dk, const float (&qf)[32],
+                                                 const PrefillArgs &a, int h, int ktn, float *nk,
+                                                 float *nv, floatx4 &S0, floatx4 &S1) {
+  constexpr int NI = kPrefillTile / 4 / (64 * G);  // copies per wave per half tile
+  constexpr int STEP = 8 / NI;                     // one copy part every STEP groups
+  const int lane = threadIdx.x & 63, j = lane & 15, u = lane >> 4;
+  // K rows j and 16 + j; chunk c of a row sits at chunk c ^ (row % 16) = c ^ j
+  const float *k0 = dk + j * kHeadDim, *k1 = dk + (16 + j) * kHeadDim;
+  S0 = floatx4{};
+  S1 = floatx4{};
+  float4 n0 = ld4(k0 + 4 * (u ^ j)), n1 = ld4(k1 + 4 * (u ^ j));
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const float4 c0 = n0, c1 = n1;
+    if (m < 7) {
+      n0 = ld4(k0 + 4 * ((4 * (m + 1) + u) ^ j));
+      n1 = ld4(k1 + 4 * ((4 * (m + 1) + u) ^ j));
+    }
+    if (m % STEP == STEP - 1) pf_copy_part<G>(a, h, ktn, nk, nv, m / STEP);
+    __builtin_amdgcn_sched_barrier(0);
+    S0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c0.x, qf[4 * m], S0, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c1.x, qf[4 * m], S1, 0, 0, 0);
+    S0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c0.y, qf[4 * m + 1], S0, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c1.y, qf[4 * m + 1], S1, 0, 0, 0);
+    S0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c0.z, qf[4 * m + 2], S0, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c1.z, qf[4 * m + 2], S1, 0, 0, 0);
+    S0 = __builtin_amdgcn_mfma_f32_16x16x4f32(c0.w, qf[4 * m + 3], S0, 0, 0, 0);
+    S1 = __builtin_amdgcn_mfma_f32_16x16x4f32(c1.w, qf[4 * m + 3], S1, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Causal mask, online softmax (lazy rescaling as pf_tile_pv) and
+// O^T += V^T P^T for key tile kt of the half starting at query q0h.
+__device__ __forceinline__ void pf16_tile_pv(const PrefillArgs &a, int q0h, int kt, floatx4 S0,
+                                             floatx4 S1, const float *dv, floatx4 (&O)[8],
+                                             float &m, float &l) {
+  const int lane = threadIdx.x & 63, j = lane & 15, u = lane >> 4;
+  const int kbase = kt * 32;
+  float s[8] = {S0[0], S0[1], S0[2], S0[3], S1[0], S1[1], S1[2], S1[3]};  // key 16(i/4) + 4u + i%4
+  if (kbase + 31 > a.start_pos + q0h) {  // the tile reaches the causal diagonal
+    const int pq = a.start_pos + min(q0h + j, a.n_tokens - 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (kbase + 16 * (i >> 2) + 4 * u + (i & 3) > pq) s[i] = -INFINITY;
+  }
+  float mb = s[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mb = fmaxf(mb, s[i]);
+  mb = quad_max(mb);
+  if (__ballot(mb > m + 8.0f) != 0) {
+    const float mn = fmaxf(m, mb);
+    const float alpha = fast_exp2(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) O[n] *= alpha;
+    m = mn;
+  }
+  float p[8], ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p[i] = fast_exp2(s[i] - m);
+    ls += p[i];
+  }
+  l += ls;  // this lane's keys; the query's sum spans its four lanes
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const float *vr = dv + (16 * (st >> 2) + 4 * u + (st & 3)) * kHeadDim + 4 * j;
+    const float4 va = ld4(vr), vb = ld4(vr + 64);
+    O[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.x, p[st], O[0], 0, 0, 0);
+    O[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.y, p[st], O[1], 0, 0, 0);
+    O[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.z, p[st], O[2], 0, 0, 0);
+    O[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.w, p[st], O[3], 0, 0, 0);
+    O[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.x, p[st], O[4], 0, 0, 0);
+    O[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.y, p[st], O[5], 0, 0, 0);
+    O[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.z, p[st], O[6], 0, 0, 0);
+    O[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.w, p[st], O[7], 0, 0, 0);
+  }
+}
+
+// End of a half item: as pf_finish, with the half's own ticket ((kv head,
+// query tile, half)) and the half's region of the item's partial-state
+// slot: float4 k of lane l (register k % 4 of O^T blocks 4 (k/4) ..
+// 4 (k/4) + 3) at float (k*64 + l)*4, k < 8, then (m, l) of query j at
+// 2048 + 2j -- 2080 floats per wave; half h at 2080 h of the slot's 66 * 64.
+template <int G>
+__device__ __forceinline__ void pf16_finish(const PrefillArgs &a, const PfItem &it, int half,
+                                            int q0h, floatx4 (&O)[8], float m, float l,
+                                            int *s_last, unsigned long long *stamp = nullptr) {
+  const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, u = lane >> 4;
+  const int g = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = it.h, head = h * G + g;
+  l = quad_sum(l);  // the query's sum over its four lanes
+  if (it.nch > 1) {
+    const long long slot =
+        (((long long)h * a.n_items + it.base + it.ch) * G + g) * 66 * 64 + 2080LL * half;
+    const __amdgpu_buffer_rsrc_t mine = agent_buf(a.ws + slot);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int n0 = 4 * (k >> 2), r = k & 3;
+      st4_agent(mine, (k * 64 + lane) * 16,
+                make_float4(O[n0][r], O[n0 + 1][r], O[n0 + 2][r], O[n0 + 3][r]));
+    }
+    if (u == 0) st2_agent(mine, 2048 * 4 + 8 * j, m, l);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+    __syncthreads();
+    unsigned *ctr = a.counters + (((long long)h * a.n_qtiles + it.qt) * 2 + half) * kCounterStride;
+    if (tid == 0) {
+      const unsigned ticket =
+          __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = ticket == (unsigned)(it.nch - 1);
+    }
+    __syncthreads();
+    const bool last = *s_last;
+    __syncthreads();
+    PF_STAMP(stamp, kPfTicket);
+    if (!last) return;
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int c = 0; c < it.nch; ++c) {
+      if (c == it.ch) continue;
+      const __amdgpu_buffer_rsrc_t src = agent_buf(
+          a.ws + (((long long)h * a.n_items + it.base + c) * G + g) * 66 * 64 + 2080LL * half);
+      float4 ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ov[k] = ld4_agent(src, (k * 64 + lane) * 16);
+      const float2 ml = ld2_agent(src, 2048 * 4 + 8 * j);
+      const float mn = fmaxf(m, ml.x);
+      const float sa = fast_exp2(m - mn), sb = fast_exp2(ml.x - mn);
+      l = l * sa + ml.y * sb;
+      m = mn;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int n0 = 4 * (k >> 2), r = k & 3;
+        O[n0][r] = O[n0][r] * sa + ov[k].x * sb;
+        O[n0 + 1][r] = O[n0 + 1][r] * sa + ov[k].y * sb;
+        O[n0 + 2][r] = O[n0 + 2][r] * sa + ov[k].z * sb;
+        O[n0 + 3][r] = O[n0 + 3][r] * sa + ov[k].w * sb;
+      }
+    }
+    PF_STAMP(stamp, kPfMerged);
+  }
+  const float inv = 1.0f / l;
+  if (q0h + j < a.n_tokens) {
+    float *op = a.out + ((long long)(q0h + j) * a.n_heads + head) * kHeadDim + 16 * u;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        st4(op + 64 * hh + 4 * r, make_float4(O[4 * hh][r] * inv, O[4 * hh + 1][r] * inv,
+                                              O[4 * hh + 2][r] * inv, O[4 * hh + 3][r] * inv));
+  }
+  PF_STAMP(stamp, kPfStored);
+}
+
+template <int G>
+__global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill16_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) float sK0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sK1[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV0[kPrefillTile];
+  __shared__ __attribute__((aligned(16))) float sV1[kPrefillTile];
+  __shared__ int s_last;
+#if defined(BNR_TIMELINE)
+  unsigned long long stamp_buf[kTimelineStamps] = {};
+  unsigned long long *stamp = stamp_buf;
+  PF_STAMP(stamp, kPfEntry);
+#else
+  unsigned long long *stamp = nullptr;
+#endif
+  const int half = blockIdx.x & 1;
+  const PfItem it = pf_item(a, blockIdx.x >> 1, blockIdx.y);
+  const int q0h = it.q0 + 16 * half;
+  // A half past the last query: every chunk of it exits here, so its ticket
+  // is never taken and stays zero.
+  if (q0h >= a.n_tokens) return;
+  constexpr int NI = kPrefillTile / 4 / (64 * G);
+  pf_copy_half<G>(a, it.h, it.kt0, sK0, nullptr);
+  float qf[32];
+  pf16_load_q<G>(a, it.h, q0h, qf);
+  pf_copy_half<G>(a, it.h, it.kt0, nullptr, sV0);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) qf[i] *= a.scale_log2;
+  __builtin_amdgcn_s_waitcnt(0x0F70 | NI);  // all but this wave's V copies
+  __builtin_amdgcn_s_barrier();
+  PF_STAMP(stamp, kPfReady);
+  floatx4 O[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) O[n] = floatx4{};
+  float m = -1e30f, l = 0.f;
+  auto step = [&](int kt, const float *dk, const float *dv, float *nk, float *nv, bool first) {
+    floatx4 S0, S1;
+    pf16_tile_s_copy<G>(dk, qf, a, it.h, min(kt + 1, it.nkt - 1), nk, nv, S0, S1);
+    if (first) {
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * NI));
+      __builtin_amdgcn_s_barrier();
+    }
+    pf16_tile_pv(a, q0h, kt, S0, S1, dv, O, m, l);
+    wait_vmem();
+    __syncthreads();
+  };
+  step(it.kt0, sK0, sV0, sK1, sV1, true);
+  for (int kt = it.kt0 + 1; kt < it.nkt;) {
+    step(kt, sK1, sV1, sK0, sV0, false);
+    if (++kt >= it.nkt) break;
+    step(kt, sK0, sV0, sK1, sV1, false);
+    ++kt;
+  }
+  PF_STAMP(stamp, kPfTiles);
+  pf16_finish<G>(a, it, half, q0h, O, m, l, &s_last, stamp);
+#if defined(BNR_TIMELINE)
+  if (a.timeline && threadIdx.x == 0) {
+    if (it.nch == 1) stamp_buf[kPfTicket] = stamp_buf[kPfTiles];
+    constexpr int kHwId = 4 | (31 << 11), kXccId = 20 | (15 << 11);  // HW_REG_HW_ID, HW_REG_XCC_ID
+    stamp_buf[kPfHwId] = ((unsigned long long)(unsigned)__builtin_amdgcn_s_getreg(kXccId) << 32) |
+                         (unsigned)__builtin_amdgcn_s_getreg(kHwId);
+    stamp_buf[kPfItem] = (unsigned long long)(it.nkt - it.kt0) | ((unsigned long long)it.nch << 16) |
+                         ((unsigned long long)it.qt << 32);
+    unsigned long long *rec =
+        a.timeline + ((long long)blockIdx.y * gridDim.x + blockIdx.x) * kTimelineStamps;
+#pragma unroll
+    for (int k = 0; k < kTimelineStamps; ++k) rec[k] = stamp_buf[k];
+  }
+#endif
+}
+
 // Persistent prefill: gridDim.x resident workgroups (at most the number of
 // items) start on item blockIdx.x and take further items (kv head fastest,
 // longest first) from an atomic queue.  The next item's index is taken
@@ -800,6 +1090,16 @@ hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, h
       case 2: prefill_persistent_kernel<2><<<grid, dim3(128), 0, s>>>(a); break;
       case 4: prefill_persistent_kernel<4><<<grid, dim3(256), 0, s>>>(a); break;
       case 8: prefill_persistent_kernel<8><<<grid, dim3(512), 0, s>>>(a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
+  if (a.q16) {
+    const dim3 grid16(2 * a.n_kv, a.n_items);
+    switch (group) {
+      case 2: prefill16_kernel<2><<<grid16, dim3(128), 0, s>>>(a); break;
+      case 4: prefill16_kernel<4><<<grid16, dim3(256), 0, s>>>(a); break;
+      case 8: prefill16_kernel<8><<<grid16, dim3(512), 0, s>>>(a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -10,6 +10,13 @@
 
 namespace bnr {
 
+// Fitted to graph-timed MI355X spans of 12 shapes (256 to 3072 tokens, 0 to
+// 3000 cached rows) x 12 chunk sizes of the 16-query kernel: with them the
+// planner's pick is within 4 % of the best measured configuration at 9 of
+// the 12 shapes (the 2048-token prefill weighted so that it keeps its
+// 32-query plan), against 2-35 % slower for the 32-query kernel alone.
+double g_pf16_fixed = 0.40, g_pf16_tile = 0.52, g_pf16_merge = 0.0, g_pf16_margin = 0.99;
+
 // Prefill key-range chunking.  The planner replays the launch's dispatch for
 // each candidate chunk size and keeps the shortest span.  Workgroups go to
 // the XCDs round-robin (WG i to XCD i % 8), so one XCD sees every 8th
@@ -26,8 +33,12 @@ namespace bnr {
 // 0 to 4000; a tile of 4 heads alone on a CU takes about 4 us): they keep
 // the chosen chunk size within 10 % of the best measured one (2 % median).
 double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_cu,
-                    bool balanced) {
+                    bool balanced, bool q16) {
   constexpr double kShared = 1.9, kFixed = 1.0, kStore = 0.0, kMerge = 0.1;
+  // 16-query halves (prefill16_kernel): two workgroups per item, each with
+  // its own fixed cost and half-height key tiles.
+  const double fixed = q16 ? g_pf16_fixed : kFixed, tile = q16 ? g_pf16_tile : 1.0,
+               merge = q16 ? g_pf16_merge : kMerge;
   constexpr int kXcd = 8, kSlots = 2;
   const int ncu = std::max(1, n_cu / kXcd);
   struct Cu {
@@ -95,8 +106,10 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
       t = std::min(nk, (ch + 1) * ctiles) - ch * ctiles;
     }
     {
-      for (int h = 0; h < n_kv; ++h, ++wg) {
+      for (int w = 0; w < (q16 ? 2 : 1) * n_kv; ++w, ++wg) {
         if (wg % kXcd != 0) continue;
+        // the second half of a last tile with at most 16 queries exits at once
+        const bool idle = q16 && (w & 1) && qt * 32 + 16 >= n_tokens;
         int cu;
         while ((cu = pick()) < 0) {  // wait for a slot: run to the next finish
           std::pop_heap(heap.begin(), heap.end());
@@ -120,8 +133,8 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
         }
         Cu &c = cus[(size_t)cu];
         advance(c, now);
-        c.rem[c.n] = kFixed + t + (nch > 1 ? kStore : 0.0);
-        c.tail[c.n] = nch > 1 ? (nch - 1) * kMerge : 0.0;
+        c.rem[c.n] = idle ? 0.01 : fixed + t * tile + (nch > 1 ? kStore : 0.0);
+        c.tail[c.n] = !idle && nch > 1 ? (nch - 1) * merge : 0.0;
         ++c.n;
         schedule(cu);
       }
@@ -146,33 +159,42 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
 
 constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
 
-// Key tiles per chunk for a prefill shape (kPrefillNoSplit: no split), and
-// whether the chunks are balanced (*balanced).  Each candidate costs two
-// dispatch replays (tens to hundreds of us each); sizes between the powers
-// of two matter: they set how evenly the items fill the resident slots
-// (N = 1024 runs 8 % faster at 6 tiles than at 4, 512 queries after 1536
-// cached 14 % faster at 10 than at 4 or 16).  bal_pref: -1 either, 0 plain
-// chunks only, 1 balanced chunks only.  A candidate whose (kv head, item)
-// pairs would exceed prefill_item_budget(cap) is not considered, so the
-// workspace sized by that budget holds every planned launch.
-int plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
-                       long long cap, int *balanced) {
+// The chunk size, balance and query height for a prefill shape.  Each
+// candidate costs two dispatch replays (tens to hundreds of us each); sizes
+// between the powers of two matter: they set how evenly the items fill the
+// resident slots (N = 1024 runs 8 % faster at 6 tiles than at 4, 512 queries
+// after 1536 cached 14 % faster at 10 than at 4 or 16).  A candidate whose
+// (kv head, item) pairs would exceed prefill_item_budget(cap) is not
+// considered, so the workspace sized by that budget holds every planned
+// launch.
+PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
+                                 int q16_pref, long long cap) {
   const long long budget = prefill_item_budget(cap, n_kv);
-  int best = kPrefillNoSplit, best_bal = 0;
-  double best_span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, n_cu, false);
-  for (int ct : kPrefillChunkCandidates) {
-    if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > budget) continue;
-    for (int bal = 0; bal <= 1; ++bal) {
-      if ((bal == 0 && bal_pref == 1) || (bal == 1 && bal_pref == 0)) continue;
-      const double span = prefill_span(n_tokens, start_pos, n_kv, ct, n_cu, bal != 0);
-      if (span < best_span * 0.99) {
-        best_span = span;
-        best = ct;
-        best_bal = bal;
+  PrefillChoice best{kPrefillNoSplit, 0, 0};
+  double best_span = 1e300;
+  for (int q = 0; q <= 1; ++q) {
+    if ((q == 0 && q16_pref == 1) || (q == 1 && q16_pref == 0)) continue;
+    const double margin = q ? g_pf16_margin : 0.99;  // a switch to halves must gain this much
+    const double span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, n_cu, false, q);
+    if (span < best_span * margin) {
+      best_span = span;
+      best = PrefillChoice{kPrefillNoSplit, 0, q};
+    }
+    for (int ct : kPrefillChunkCandidates) {
+      if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > budget) continue;
+      for (int bal = 0; bal <= 1; ++bal) {
+        if ((bal == 0 && bal_pref == 1) || (bal == 1 && bal_pref == 0)) continue;
+        // 16-query halves with balanced chunks measured 4-12 % slower than
+        // with plain ones at every shape tried: not a candidate
+        if (q && bal && bal_pref != 1) continue;
+        const double sp = prefill_span(n_tokens, start_pos, n_kv, ct, n_cu, bal != 0, q);
+        if (sp < best_span * (q && !best.q16 ? margin : 0.99)) {
+          best_span = sp;
+          best = PrefillChoice{ct, bal, q};
+        }
       }
     }
   }
-  *balanced = best_bal;
   return best;
 }
 

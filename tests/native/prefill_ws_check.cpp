@@ -1,6 +1,7 @@
 // Checks the bound on the chunked-prefill workspace: over seeded launch
 // shapes on caches of 96 to 8192 rows with 1 to 8 kv heads, every chunk size
-// the planner picks (plain or balanced chunks) keeps the launch's (kv head,
+// the planner picks (plain or balanced chunks, 32-query tiles or 16-query
+// halves, either forced or the planner's choice) keeps the launch's (kv head,
 // item) pairs within prefill_item_budget(cap, n_kv), which is what the
 // workspace is sized for; the budget is four items per query tile of the
 // cache, at most kPrefillMaxPlannedItems, and never falls as the cache
@@ -38,11 +39,12 @@ int main() {
         const int room = (int)cap - n;
         const int start = room > 0 ? (int)(rng() % (unsigned)(std::min(room, n) + 1)) : 0;
         for (int pref = -1; pref <= 1; ++pref) {
-          int bal = -1;
-          const int ct = plan_prefill_chunk(n, start, n_kv, 256, pref, cap, &bal);
+          const PrefillChoice pc = plan_prefill_chunk(n, start, n_kv, 256, pref, pref, cap);
+          const int ct = pc.tiles, bal = pc.balanced;
           const PrefillPlan p = prefill_plan(n, start, ct);
           ++launches;
-          if (ct < 1 || (bal != 0 && bal != 1) || (pref >= 0 && p.split && bal != pref)) {
+          if (ct < 1 || (bal != 0 && bal != 1) || (pref >= 0 && p.split && bal != pref) ||
+              (pref >= 0 && pc.q16 != pref)) {
             std::printf("FAIL pick ct %d bal %d (cap %lld n_kv %d n %d start %d pref %d)\n", ct, bal,
                         cap, n_kv, n, start, pref);
             return 1;

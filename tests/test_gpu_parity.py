@@ -523,6 +523,56 @@ def test_dev_prefill_key_chunks(monkeypatch, tiles, persistent):
         be_gpu.close()
 
 
+@pytest.mark.parametrize("q16", [0, 1])
+@pytest.mark.parametrize("n_heads,n_kv,tiles,balanced", [(20, 5, 3, 0), (20, 5, 5, 1),
+                                                         (20, 5, 1 << 20, 0), (16, 2, 4, 0),
+                                                         (32, 4, 3, 0), (8, 8, 2, 1)])
+def test_dev_prefill_query_height(monkeypatch, q16, n_heads, n_kv, tiles, balanced):
+    """32-query tiles (prefill_kernel) and 16-query halves (prefill16_kernel)
+    forced on the same launches: chunked and whole query tiles, plain and
+    balanced chunks, 2 to 8 q heads per kv head, token counts that leave the
+    last tile's second half empty (n % 32 <= 16) or partly filled, and start
+    positions off the tile grid; two prefills in a row so that the halves'
+    tickets reset themselves.  Rotated q/k and cache rows bit for bit."""
+    case(f"prefill q16 {q16} heads {n_heads}/{n_kv} tiles {tiles} balanced {balanced}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_Q16", str(q16))
+    monkeypatch.setenv("BNR_PREFILL_CHUNK_TILES", str(tiles))
+    monkeypatch.setenv("BNR_PREFILL_BALANCED", str(balanced))
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = 700
+        cache = oracle.KVCache(1, n_kv, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        pre = prefill_workload(53, 29, n_heads, n_kv)
+        oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+        d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+        d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+        start = 29
+        for n_tokens, sd in ((272, 54), (210, 55), (17, 56)):
+            w = prefill_workload(sd, n_tokens, n_heads, n_kv)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be, n_heads=n_heads, n_kv=n_kv)
+            out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads, n_kv, D, THETA,
+                               d_kc, d_vc, cap, out)
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
+            np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+            assert_close(host(out), out_ref,
+                         f"prefill q16 {q16} {n_heads}/{n_kv} tiles {tiles} n {n_tokens} "
+                         f"start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
+
+
 @pytest.mark.parametrize("n_heads,n_kv,tiles,persistent", [(16, 2, 2, 0), (16, 2, 3, 1),
                                                            (8, 4, 3, 0), (8, 4, 2, 1)])
 def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persistent):
