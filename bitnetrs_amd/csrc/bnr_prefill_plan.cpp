@@ -11,11 +11,12 @@
 namespace bnr {
 
 // Fitted to graph-timed MI355X spans of 12 shapes (256 to 3072 tokens, 0 to
-// 3000 cached rows) x 12 chunk sizes of the 16-query kernel: with them the
-// planner's pick is within 4 % of the best measured configuration at 9 of
-// the 12 shapes (the 2048-token prefill weighted so that it keeps its
-// 32-query plan), against 2-35 % slower for the 32-query kernel alone.
-double g_pf16_fixed = 0.40, g_pf16_tile = 0.52, g_pf16_merge = 0.0, g_pf16_margin = 0.99;
+// 3000 cached rows) x 12 chunk sizes of the 16-query kernel, the 1024- and
+// 2048-token prefills from an empty cache weighted 5x: the planner's pick is
+// the best measured configuration at 7 of the 12 shapes, within 5 % at 3
+// more and within 12 % at all, where the 32-query kernel alone is 2-54 %
+// slower than the best at 9 of them.
+double g_pf16_fixed = 0.40, g_pf16_tile = 0.52, g_pf16_merge = 0.05, g_pf16_margin = 0.99;
 
 // Prefill key-range chunking.  The planner replays the launch's dispatch for
 // each candidate chunk size and keeps the shortest span.  Workgroups go to
