@@ -163,9 +163,10 @@ void fingerprint(const uint8_t *p, size_t len, uint8_t *out) {
 constexpr size_t kMaxWeightMirrors = 1024;
 
 struct PrefillPlanEntry {
-  int n_tokens, start_pos, n_kv;
+  int n_tokens, start_pos, n_kv, pair_pref;
   long long cap;
   PrefillChoice choice;
+  PairPlan pairs;  // choice.pairs
 };
 
 struct DeviceGuard {
@@ -277,6 +278,7 @@ struct bnr_ctx {
   int pf_sk_wgs = 0;              // stream-K workgroups (0: every resident slot)
   int pf_q16 = -1;                // 16-query halves (prefill16_kernel): -1 planner, 0 never, 1 always
   int pf_balanced = -1;           // balanced key chunks: -1 planner, 0 never, 1 always
+  int pf_pair = -1;               // paired 16-query launches: -1 planner (4 q heads per kv head), 0 never, 1 where possible
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
 
@@ -501,17 +503,22 @@ void free_ws(DecodeWs &w) {
 DecodeWs &ws_for(bnr_ctx *c, hipStream_t s) { return s == c->stream ? c->hws : c->dws; }
 
 // The planner's choice for a prefill shape, remembered for the last 16
-// shapes (planning replays the dispatch for every candidate).
-PrefillChoice plan_prefill_cached(bnr_ctx *c, int n_tokens, int start_pos, int n_kv,
-                                  long long cap) {
+// shapes (planning replays the dispatch for every candidate).  Paired
+// launches are planned for 4 q heads per kv head (two workgroups of the
+// 16-query kernel per CU) unless forced.
+PrefillPlanEntry plan_prefill_cached(bnr_ctx *c, int n_tokens, int start_pos, int n_kv, int group,
+                                     long long cap) {
+  const int pair_pref = c->pf_pair == 1 ? 1 : (c->pf_pair == -1 && group == 4 ? -1 : 0);
   for (const PrefillPlanEntry &e : c->pf_plans)
-    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv && e.cap == cap)
-      return e.choice;
-  const PrefillChoice ch =
-      plan_prefill_chunk(n_tokens, start_pos, n_kv, c->n_cu, c->pf_balanced, c->pf_q16, cap);
+    if (e.n_tokens == n_tokens && e.start_pos == start_pos && e.n_kv == n_kv && e.cap == cap &&
+        e.pair_pref == pair_pref)
+      return e;
+  PrefillPlanEntry e{n_tokens, start_pos, n_kv, pair_pref, cap, PrefillChoice{}, PairPlan{}};
+  e.choice = plan_prefill_chunk(n_tokens, start_pos, n_kv, c->n_cu, c->pf_balanced, c->pf_q16,
+                                cap, pair_pref, &e.pairs);
   if (c->pf_plans.size() >= 16) c->pf_plans.erase(c->pf_plans.begin());
-  c->pf_plans.push_back(PrefillPlanEntry{n_tokens, start_pos, n_kv, cap, ch});
-  return ch;
+  c->pf_plans.push_back(e);
+  return e;
 }
 
 // RopeCache::new (bitnet-cpu/src/rope.rs:100-153) on the host: same f32
@@ -896,6 +903,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (const char *v = std::getenv("BNR_PREFILL_SK_WGS")) c->pf_sk_wgs = std::max(atoi(v), 0);
   if (const char *v = std::getenv("BNR_PREFILL_Q16")) c->pf_q16 = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_BALANCED")) c->pf_balanced = std::min(1, std::max(-1, atoi(v)));
+  if (const char *v = std::getenv("BNR_PREFILL_PAIR")) c->pf_pair = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_MODE")) {
     const int m = atoi(v);
     if (m >= kPrefillGrid && m <= kPrefillAuto) c->pf_mode = m;
@@ -1708,17 +1716,24 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
     pa.timeline = c->timeline;
     const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
     const bool streamk = prefill_streamk(c, n_tokens, start_pos);
+    int pair_slots = -1;  // a paired launch: its partial-state slots per kv head
     if (!streamk) {
       if (c->pf_chunk_tiles > 0) {
         pa.chunk_tiles = c->pf_chunk_tiles;
         pa.balanced = c->pf_balanced == 1;
         pa.q16 = c->pf_q16 == 1;
       } else {
-        const PrefillChoice ch = plan_prefill_cached(c, (int)n_tokens, (int)start_pos,
-                                                     (int)n_kv_heads, (long long)cap);
-        pa.chunk_tiles = ch.tiles;
-        pa.balanced = ch.balanced;
-        pa.q16 = ch.q16;
+        const PrefillPlanEntry e = plan_prefill_cached(c, (int)n_tokens, (int)start_pos,
+                                                       (int)n_kv_heads, group, (long long)cap);
+        pa.chunk_tiles = e.choice.tiles;
+        pa.balanced = e.choice.balanced;
+        pa.q16 = e.choice.q16;
+        if (e.choice.pairs) {
+          pa.pair_bins = e.pairs.bins;
+          pa.pair_cu = c->n_cu;
+          std::memcpy(pa.pair_piece, e.pairs.piece, sizeof(pa.pair_piece));
+          pair_slots = e.pairs.n_slots;
+        }
       }
     } else {
       pa.chunk_tiles = kPrefillNoSplit;
@@ -1761,12 +1776,15 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
       HIP_TRY(launch_prefill_streamk(pa, group, wgs, s), "prefill launch");
       return set_ok();
     }
-    if (plan.split) {
+    if (plan.split || pair_slots >= 0) {
       pa.ws = c->pf_ws;
       pa.counters = c->pf_counters;
     }
+    // slots of the pieces' partial states (within the reservation above:
+    // the planner keeps them to prefill_item_budget)
+    if (pair_slots >= 0) pa.n_items = std::max(pair_slots, 1);
     int pwgs = 0;
-    if (c->pf_mode == kPrefillQueue) pa.q16 = 0;  // the persistent kernel runs whole tiles
+    if (c->pf_mode == kPrefillQueue) pa.q16 = pa.pair_bins = 0;  // the persistent kernel runs whole tiles
     if (c->pf_mode == kPrefillQueue) {
       st = ensure_zeroed(&c->pf_queue, &c->n_pf_queue, 2 * kCounterStride);
       if (st) return st;

@@ -182,6 +182,9 @@ hipError_t launch_stream_read_shape(const void *a, long long a_bytes, const void
                                     long long b_bytes, int threads, int loads, bool nt,
                                     hipStream_t s);
 
+// Bins per kv head of a paired 16-query prefill launch (PrefillArgs).
+constexpr int kMaxPairBins = 64;
+
 // Causal flash prefill (head_dim 128, fp32 MFMA): query i of the n_tokens
 // (position start_pos + i) attends cache rows 0..start_pos+i.
 struct PrefillArgs {
@@ -218,6 +221,17 @@ struct PrefillArgs {
   // (prefill16_kernel; grid x = 2 n_kv); counters then hold one ticket per
   // (kv head, query tile, half).
   int q16;
+  // Paired launch of the 16-query kernel (pair_bins > 0, q16 = 1): a 1-D grid
+  // of 2 * pair_cu workgroups.  Workgroup i runs piece i / pair_cu of bin
+  // b = (i % pair_cu) / n_kv for kv head (i % pair_cu) % n_kv; a bin past
+  // pair_bins or a piece of zero length exits at once.  A piece is a key
+  // range of one 16-query unit (pf16_pair_piece has the encoding); the plan
+  // puts at most two pieces in a bin so that they share a CU: on an idle
+  // device the dispatcher gives workgroups i and i + (CU count) the same CU,
+  // the first one first.  n_items is then the partial-state slots per kv
+  // head (base + ch of a piece; both halves of a query tile share a slot).
+  int pair_bins, pair_cu;
+  unsigned pair_piece[2 * kMaxPairBins][2];
   // Stream-K launch (sk_units > 0): units = (kv head, query tile, key tile)
   // tile products in that order, sk_per_head of them per kv head; the
   // launch's workgroups take equal runs of them.  ws then holds two partial
@@ -229,6 +243,8 @@ struct PrefillArgs {
   // otherwise.
   unsigned long long *timeline;
 };
+// Kernel arguments are passed by value: keep them within 4 KB.
+static_assert(sizeof(PrefillArgs) <= 4096, "PrefillArgs exceeds the kernel argument limit");
 // Words of a prefill workgroup's timeline record: 100 MHz s_memrealtime
 // stamps at entry, Q and first K/V tile in LDS, last key tile done, partial
 // state stored and ticket taken (split query tiles; else = key tiles done),
@@ -431,14 +447,38 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles, int n_cu,
 // (kPrefillNoSplit: none), balanced chunks, 16-query halves.
 struct PrefillChoice {
   int tiles, balanced, q16;
+  int pairs;  // a paired 16-query launch (PairPlan) instead of chunks
 };
-// bal_pref / q16_pref: -1 either, 0 never, 1 always.
+// bal_pref / q16_pref / pair_pref: -1 either, 0 never, 1 always (a paired
+// launch where one is possible; its plan goes to *pairs).
+struct PairPlan;
 PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
-                                 int q16_pref, long long cap);
+                                 int q16_pref, long long cap, int pair_pref = 0,
+                                 PairPlan *pairs = nullptr);
+
+// Paired plan of a 16-query launch that fits one dispatch round: the key
+// tiles of every 16-query unit (queries 16 u .. 16 u + 15 attend key tiles
+// 0 .. nk(u) - 1) are cut into pieces and the pieces packed into at most
+// min(n_cu / n_kv, kMaxPairBins) bins of at most two pieces and tau key
+// tiles each, tau as small as the packing allows.  piece[2 b + s] is piece
+// s of bin b (s = 0 the longer one, started first):
+//   w0 = kt0 | qt << 16 | half << 31        (unit u = 2 qt + half)
+//   w1 = len | ch << 8 | nch << 16 | base << 24
+// with len = 0 for an empty slot.  The chunks of a unit are its pieces in
+// key order; a query tile's split units use slots base .. base + nch - 1
+// (n_slots per kv head).  `span` is the modelled span in prefill_span's
+// units.
+struct PairPlan {
+  int bins = 0, tau = 0, n_slots = 0;
+  double span = 0.0;
+  unsigned piece[2 * kMaxPairBins][2] = {};
+};
+bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long long item_budget,
+                        PairPlan &p);
 // Constants of the 16-query halves in the span model (fixed cost, key tile,
 // merge per extra chunk; a 32-query tile alone on a CU takes 1) and the
 // span ratio below which the planner switches to them.
-extern double g_pf16_fixed, g_pf16_tile, g_pf16_merge, g_pf16_margin;
+extern double g_pf16_fixed, g_pf16_tile, g_pf16_merge, g_pf16_margin, g_pair_margin;
 long long prefill_item_budget(long long cap, int n_kv);
 constexpr long long kPrefillMaxPlannedItems = 8192;
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.

@@ -111,48 +111,52 @@ __device__ __forceinline__ PfItem pf_item(const PrefillArgs &a, int h, int y) {
 
 // Copy of key tile kt of kv head h: copy j of wave w fills rows 2J, 2J+1
 // (J = w*NI + j); lane l takes row 2J + l/32, LDS chunk l%32.  Rows past the
-// last cached one repeat it (their keys are masked for every query).
-template <int G>
-__device__ __forceinline__ void pf_copy_part(const PrefillArgs &a, int h, int kt, float *dk,
-                                             float *dv, int j) {
+// last cached one repeat it (their keys are masked for every query).  The
+// K half (CK), the V half (CV) or both.
+template <int G, bool CK, bool CV>
+__device__ __forceinline__ void pf_copy_rows(const PrefillArgs &a, int h, int kt, float *dk,
+                                             float *dv) {
   constexpr int NI = kPrefillTile / 4 / (64 * G);  // 1 KB copies per wave per tile
   const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int last_row = a.start_pos + a.n_tokens - 1;
   const float *kc = a.k_cache + h * a.kv_stride;
   const float *vc = a.v_cache + h * a.kv_stride;
-  const int J = wave * NI + j;
-  const int r = 2 * J + hl, p = col;
-  const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
-  dma16(kc + grow + 4 * (p ^ (r & 15)), dk + J * 256);
-  dma16(vc + grow + 4 * p, dv + J * 256);
+  if (kt * 32 + 31 <= last_row) {
+    // A whole cached tile (one uniform test per tile): the tile's address is
+    // uniform and the lane's part a 32-bit offset, so the copies take scalar
+    // base + vector offset addressing, no 64-bit vector arithmetic.
+    const char *kb = (const char *)(kc + (long long)kt * 32 * kHeadDim);
+    const char *vb = (const char *)(vc + (long long)kt * 32 * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int J = wave * NI + j;
+      const int r = 2 * J + hl;
+      if (CK) dma16((const float *)(kb + (unsigned)(r * kHeadDim + 4 * (col ^ (r & 15))) * 4u), dk + J * 256);
+      if (CV) dma16((const float *)(vb + (unsigned)(r * kHeadDim + 4 * col) * 4u), dv + J * 256);
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int J = wave * NI + j;
+    const int r = 2 * J + hl;
+    const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
+    if (CK) dma16(kc + grow + 4 * (col ^ (r & 15)), dk + J * 256);
+    if (CV) dma16(vc + grow + 4 * col, dv + J * 256);
+  }
 }
 // The K half (dv null) or the V half (dk null) of a tile's copies.
 template <int G>
 __device__ __forceinline__ void pf_copy_half(const PrefillArgs &a, int h, int kt, float *dk,
                                              float *dv) {
-  constexpr int NI = kPrefillTile / 4 / (64 * G);
-  const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int last_row = a.start_pos + a.n_tokens - 1;
-  const float *src = (dk ? a.k_cache : a.v_cache) + h * a.kv_stride;
-#pragma unroll
-  for (int j = 0; j < NI; ++j) {
-    const int J = wave * NI + j;
-    const int r = 2 * J + hl, p = col;
-    const long long grow = (long long)min(kt * 32 + r, last_row) * kHeadDim;
-    if (dk)
-      dma16(src + grow + 4 * (p ^ (r & 15)), dk + J * 256);
-    else
-      dma16(src + grow + 4 * p, dv + J * 256);
-  }
+  if (dk) pf_copy_rows<G, true, false>(a, h, kt, dk, nullptr);
+  else pf_copy_rows<G, false, true>(a, h, kt, nullptr, dv);
 }
 template <int G>
 __device__ __forceinline__ void pf_copy_tile(const PrefillArgs &a, int h, int kt, float *dk,
                                              float *dv) {
-  constexpr int NI = kPrefillTile / 4 / (64 * G);
-#pragma unroll
-  for (int j = 0; j < NI; ++j) pf_copy_part<G>(a, h, kt, dk, dv, j);
+  pf_copy_rows<G, true, true>(a, h, kt, dk, dv);
 }
 
 // This lane's Q fragment (dims 64*hl .. 64*hl+63 of its query, the wave's
@@ -232,8 +236,7 @@ __device__ __forceinline__ floatx16 pf_tile_s_copy(const float *dk, const float 
     S = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * i + 3], S, 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   }
-#pragma unroll
-  for (int j = 0; j < NI; ++j) pf_copy_part<G>(a, h, ktn, nk, nv, j);
+  pf_copy_tile<G>(a, h, ktn, nk, nv);
   return S;
 }
 
@@ -535,8 +538,7 @@ __device__ __forceinline__ void pf16_tile_s_copy(const float *dk, const float (&
   // compiler waits for LDS reads with lgkmcnt(0) only, so a copy among the
   // K reads would hold every group of products to its own reads (measured:
   // 3.97 us per tile with the copies before the products, 3.76 after).
-#pragma unroll
-  for (int i = 0; i < NI; ++i) pf_copy_part<G>(a, h, ktn, nk, nv, i);
+  pf_copy_tile<G>(a, h, ktn, nk, nv);
 }
 
 // Causal mask, online softmax (lazy rescaling as pf_tile_pv) and
@@ -669,6 +671,28 @@ __device__ __forceinline__ void pf16_finish(const PrefillArgs &a, const PfItem &
   PF_STAMP(stamp, kPfStored);
 }
 
+// Piece of a paired launch for this workgroup (PrefillArgs::pair_piece):
+// false for a workgroup past the plan's bins or on an empty slot.
+__device__ __forceinline__ bool pf16_pair_piece(const PrefillArgs &a, PfItem &it, int &half) {
+  const int cu = (int)blockIdx.x % a.pair_cu, slot = (int)blockIdx.x / a.pair_cu;
+  const int bin = cu / a.n_kv;
+  if (bin >= a.pair_bins) return false;
+  const unsigned w0 = a.pair_piece[2 * bin + slot][0], w1 = a.pair_piece[2 * bin + slot][1];
+  const int len = (int)(w1 & 255u);
+  if (len == 0) return false;
+  it.h = cu - bin * a.n_kv;
+  it.y = 2 * bin + slot;
+  it.kt0 = (int)(w0 & 0xFFFFu);
+  it.nkt = it.kt0 + len;
+  it.qt = (int)((w0 >> 16) & 0x7FFFu);
+  it.q0 = it.qt * 32;
+  half = (int)(w0 >> 31);
+  it.ch = (int)((w1 >> 8) & 255u);
+  it.nch = (int)((w1 >> 16) & 255u);
+  it.base = (int)(w1 >> 24);
+  return true;
+}
+
 template <int G>
 __global__ __launch_bounds__(64 * G) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill16_kernel(PrefillArgs a) {
@@ -684,8 +708,14 @@ void prefill16_kernel(PrefillArgs a) {
 #else
   unsigned long long *stamp = nullptr;
 #endif
-  const int half = blockIdx.x & 1;
-  const PfItem it = pf_item(a, blockIdx.x >> 1, blockIdx.y);
+  int half;
+  PfItem it;
+  if (a.pair_bins > 0) {
+    if (!pf16_pair_piece(a, it, half)) return;
+  } else {
+    half = blockIdx.x & 1;
+    it = pf_item(a, blockIdx.x >> 1, blockIdx.y);
+  }
   const int q0h = it.q0 + 16 * half;
   // A half past the last query: every chunk of it exits here, so its ticket
   // is never taken and stays zero.
@@ -1114,7 +1144,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int group, int persistent_wgs, h
     return hipGetLastError();
   }
   if (a.q16) {
-    const dim3 grid16(2 * a.n_kv, a.n_items);
+    const dim3 grid16 = a.pair_bins > 0 ? dim3(2 * a.pair_cu) : dim3(2 * a.n_kv, a.n_items);
     switch (group) {
       case 2: prefill16_kernel<2><<<grid16, dim3(128), 0, s>>>(a); break;
       case 4: prefill16_kernel<4><<<grid16, dim3(256), 0, s>>>(a); break;

@@ -160,6 +160,162 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
 
 constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
 
+// Span ratio below which the planner takes a paired launch.  The bin model
+// overrates the pairs' span: graph-timed on MI355X (20/5 heads) they beat
+// the planned chunks where the modelled ratio is up to 1.03 (512 tokens
+// 24.4 vs 26.0 us, 1536 tokens 114.5 vs 120.5 us, 768 tokens 37.2 vs 41.7
+// us, 1024 tokens 57.8-58.1 vs 59.5-60.7 us) and lose by 2 % at 1.023 (256
+// after 1024 cached rows).
+double g_pair_margin = 1.03;
+
+namespace {
+
+struct PairPiece {
+  int unit, kt0, len;
+};
+struct PairBin {
+  PairPiece p[2];
+  int n, sum;
+};
+
+// Pieces of the units (nk[u] key tiles each) packed into bins of at most
+// two pieces and tau key tiles.  Units shorter than thr go whole, the
+// longest with the shortest while both fit, else the longest alone; the
+// others form one chain, longest first, cut into bins that close when full
+// or when they hold two pieces.  False when a bin would exceed max_bins or
+// a whole unit tau.
+bool pair_pack(const std::vector<int> &nk, int tau, int thr, int max_bins,
+               std::vector<PairBin> &bins) {
+  bins.clear();
+  std::vector<int> small, large;
+  for (int u = 0; u < (int)nk.size(); ++u) (nk[u] < thr ? small : large).push_back(u);
+  std::stable_sort(small.begin(), small.end(), [&](int a, int b) { return nk[a] < nk[b]; });
+  std::stable_sort(large.begin(), large.end(), [&](int a, int b) { return nk[a] > nk[b]; });
+  for (int i = 0, j = (int)small.size() - 1; i <= j;) {
+    const int uj = small[(size_t)j];
+    if (nk[uj] > tau || (int)bins.size() >= max_bins) return false;
+    PairBin b{};
+    b.p[b.n++] = PairPiece{uj, 0, nk[uj]};
+    b.sum = nk[uj];
+    if (i < j && nk[small[(size_t)i]] + nk[uj] <= tau) {
+      const int ui = small[(size_t)i++];
+      b.p[b.n++] = PairPiece{ui, 0, nk[ui]};
+      b.sum += nk[ui];
+    }
+    --j;
+    bins.push_back(b);
+  }
+  PairBin cur{};
+  for (int u : large) {
+    for (int k0 = 0; k0 < nk[u];) {
+      const int take = std::min(nk[u] - k0, tau - cur.sum);
+      cur.p[cur.n++] = PairPiece{u, k0, take};
+      cur.sum += take;
+      k0 += take;
+      if (cur.sum == tau || cur.n == 2) {
+        if ((int)bins.size() >= max_bins) return false;
+        bins.push_back(cur);
+        cur = PairBin{};
+      }
+    }
+  }
+  if (cur.n) {
+    if ((int)bins.size() >= max_bins) return false;
+    bins.push_back(cur);
+  }
+  return true;
+}
+
+}  // namespace
+
+// The paired plan (see PairPlan).  For each tau from the mean bin load up,
+// every threshold between pairing whole units and cutting the chain is
+// packed, the packing with the fewest pieces kept; the first tau whose
+// packing fits the bins and the partial-state slots wins.  Its span is
+// prefill_span's CU model applied to each bin: the two pieces side by side,
+// the longer finishing alone, plus the merge of a split unit.
+bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long long item_budget,
+                        PairPlan &p) {
+  p = PairPlan{};
+  if (n_tokens <= 0 || n_kv <= 0 || start_pos < 0) return false;
+  const int max_bins = std::min(n_cu / n_kv, kMaxPairBins);
+  const int nu = (n_tokens + 15) / 16;
+  if (max_bins <= 0 || nu > 2 * max_bins) return false;
+  const long long last_row = (long long)start_pos + n_tokens - 1;
+  if (last_row / 32 + 1 > 65535) return false;  // kt0 + len in 16 bits
+  std::vector<int> nk((size_t)nu);
+  long long S = 0;
+  for (int u = 0; u < nu; ++u) {
+    nk[(size_t)u] = (int)(std::min<long long>(start_pos + 16LL * u + 15, last_row) / 32 + 1);
+    S += nk[(size_t)u];
+  }
+  std::vector<PairBin> bins, best;
+  std::vector<int> thr;
+  for (int tau = (int)std::max<long long>(1, (S + max_bins - 1) / max_bins); tau <= 255; ++tau) {
+    thr.assign({1, tau + 1});
+    for (int v : nk)
+      if (v <= tau) thr.push_back(v);
+    std::sort(thr.begin(), thr.end());
+    thr.erase(std::unique(thr.begin(), thr.end()), thr.end());
+    int best_pieces = 1 << 30;
+    best.clear();
+    for (int t : thr) {
+      if (!pair_pack(nk, tau, t, max_bins, bins)) continue;
+      int pieces = 0;
+      for (const PairBin &b : bins) pieces += b.n;
+      if (pieces < best_pieces) {
+        best_pieces = pieces;
+        best = bins;
+      }
+    }
+    if (best.empty()) continue;
+    // chunks of each unit in key order
+    std::vector<int> nch((size_t)nu, 0);
+    for (const PairBin &b : best)
+      for (int k = 0; k < b.n; ++k) ++nch[(size_t)b.p[k].unit];
+    // slots of the split query tiles (both halves share a slot index)
+    const int nqt = (n_tokens + 31) / 32;
+    std::vector<int> base((size_t)nqt, 0);
+    int n_slots = 0;
+    for (int qt = 0; qt < nqt; ++qt) {
+      const int m = std::max(nch[(size_t)(2 * qt)], 2 * qt + 1 < nu ? nch[(size_t)(2 * qt + 1)] : 0);
+      base[(size_t)qt] = n_slots;
+      if (m > 1) n_slots += m;
+    }
+    if (n_slots > 256 || (long long)n_slots * n_kv > item_budget) continue;
+    p.bins = (int)best.size();
+    p.tau = tau;
+    p.n_slots = n_slots;
+    double span = 0.0;
+    constexpr double kShared = 1.9;
+    for (size_t b = 0; b < best.size(); ++b) {
+      PairBin bin = best[b];
+      if (bin.n == 2 && bin.p[1].len > bin.p[0].len) std::swap(bin.p[0], bin.p[1]);
+      double w[2] = {0.0, 0.0}, tail = 0.0;
+      for (int k = 0; k < bin.n; ++k) {
+        const PairPiece &pc = bin.p[k];
+        const int u = pc.unit, qt = u / 2, half = u & 1;
+        int ch = 0;  // pieces of the unit before this one
+        for (const PairBin &o : best)
+          for (int j = 0; j < o.n; ++j)
+            if (o.p[j].unit == u && o.p[j].kt0 < pc.kt0) ++ch;
+        const int n = nch[(size_t)u];
+        p.piece[2 * b + k][0] = (unsigned)pc.kt0 | (unsigned)qt << 16 | (unsigned)half << 31;
+        p.piece[2 * b + k][1] = (unsigned)pc.len | (unsigned)ch << 8 | (unsigned)n << 16 |
+                                (unsigned)(n > 1 ? base[(size_t)qt] : 0) << 24;
+        w[k] = g_pf16_fixed + pc.len * g_pf16_tile;
+        if (n > 1) tail = std::max(tail, (n - 1) * g_pf16_merge);
+      }
+      const double a = std::min(w[0], w[1]), c = std::max(w[0], w[1]);
+      span = std::max(span, (bin.n == 2 ? a * kShared + (c - a) : c) + tail);
+    }
+    p.span = span;
+    return true;
+  }
+  p = PairPlan{};
+  return false;
+}
+
 // The chunk size, balance and query height for a prefill shape.  Each
 // candidate costs two dispatch replays (tens to hundreds of us each); sizes
 // between the powers of two matter: they set how evenly the items fill the
@@ -169,9 +325,9 @@ constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20,
 // considered, so the workspace sized by that budget holds every planned
 // launch.
 PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
-                                 int q16_pref, long long cap) {
+                                 int q16_pref, long long cap, int pair_pref, PairPlan *pairs) {
   const long long budget = prefill_item_budget(cap, n_kv);
-  PrefillChoice best{kPrefillNoSplit, 0, 0};
+  PrefillChoice best{kPrefillNoSplit, 0, 0, 0};
   double best_span = 1e300;
   for (int q = 0; q <= 1; ++q) {
     if ((q == 0 && q16_pref == 1) || (q == 1 && q16_pref == 0)) continue;
@@ -179,7 +335,7 @@ PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu
     const double span = prefill_span(n_tokens, start_pos, n_kv, kPrefillNoSplit, n_cu, false, q);
     if (span < best_span * margin) {
       best_span = span;
-      best = PrefillChoice{kPrefillNoSplit, 0, q};
+      best = PrefillChoice{kPrefillNoSplit, 0, q, 0};
     }
     for (int ct : kPrefillChunkCandidates) {
       if (prefill_plan(n_tokens, start_pos, ct).n_items * (long long)n_kv > budget) continue;
@@ -191,10 +347,18 @@ PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu
         const double sp = prefill_span(n_tokens, start_pos, n_kv, ct, n_cu, bal != 0, q);
         if (sp < best_span * (q && !best.q16 ? margin : 0.99)) {
           best_span = sp;
-          best = PrefillChoice{ct, bal, q};
+          best = PrefillChoice{ct, bal, q, 0};
         }
       }
     }
+  }
+  // A paired launch: one dispatch round of the 16-query kernel.
+  PairPlan pp;
+  if (pairs && pair_pref != 0 && q16_pref != 0 &&
+      plan_prefill_pairs(n_tokens, start_pos, n_kv, n_cu, budget, pp) &&
+      (pair_pref == 1 || pp.span < best_span * g_pair_margin)) {
+    *pairs = pp;
+    best = PrefillChoice{kPrefillNoSplit, 0, 1, 1};
   }
   return best;
 }

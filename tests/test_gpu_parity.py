@@ -573,6 +573,56 @@ def test_dev_prefill_query_height(monkeypatch, q16, n_heads, n_kv, tiles, balanc
         be_gpu.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv,start,lens", [(20, 5, 29, (272, 210, 17)),
+                                                     (20, 5, 0, (1024,)),
+                                                     (20, 5, 512, (512, 100)),
+                                                     (20, 5, 1500, (40, 1)),
+                                                     (16, 2, 45, (230, 33)),
+                                                     (8, 4, 3, (200, 64))])
+def test_dev_prefill_paired(monkeypatch, n_heads, n_kv, start, lens):
+    """Paired launches of the 16-query kernel forced (one dispatch round,
+    at most two key-range pieces of 16-query units per bin): whole units
+    paired, long units cut into chains of pieces whose last finisher merges
+    the others, the 30-layer stack's 1024-token shape, launches after a
+    prefix whose units are all cut, a single token, 2 to 8 q heads per kv
+    head, and launches in a row so that the tickets reset themselves.
+    Rotated q/k and cache rows bit for bit, outputs within tolerance."""
+    case(f"prefill paired heads {n_heads}/{n_kv} start {start} lens {lens}")
+    import torch
+
+    import bitnetrs_amd
+
+    monkeypatch.setenv("BNR_PREFILL_PAIR", "1")
+    be_gpu = bitnetrs_amd.HipBackend(0)
+    try:
+        cap = start + sum(lens) + 40
+        cache = oracle.KVCache(1, n_kv, D, cap)
+        be = oracle.CpuBackend()
+        d_kc = torch.zeros(n_kv, cap, D, device="cuda")
+        d_vc = torch.zeros_like(d_kc)
+        if start:
+            pre = prefill_workload(61, start, n_heads, n_kv)
+            oracle_prefill(pre, cache=cache, backend=be, n_heads=n_heads, n_kv=n_kv)
+            d_kc.copy_(torch.from_numpy(cache.k(0).reshape(n_kv, cap, D)))
+            d_vc.copy_(torch.from_numpy(cache.v(0).reshape(n_kv, cap, D)))
+        for i, n_tokens in enumerate(lens):
+            w = prefill_workload(62 + i, n_tokens, n_heads, n_kv)
+            q_ref, k_ref, cache, out_ref = oracle_prefill(w, start_pos=start, cache=cache,
+                                                          backend=be, n_heads=n_heads, n_kv=n_kv)
+            out = torch.zeros(n_tokens, n_heads * D, device="cuda")
+            q_d, k_d = dev(w["q"]), dev(w["k"])
+            be_gpu.dev_prefill(q_d, k_d, dev(w["v"]), n_tokens, start, n_heads, n_kv, D, THETA,
+                               d_kc, d_vc, cap, out)
+            np.testing.assert_array_equal(host(q_d), q_ref)
+            np.testing.assert_array_equal(host(k_d), k_ref)
+            np.testing.assert_array_equal(host(d_kc).reshape(-1), cache.k(0))
+            assert_close(host(out), out_ref,
+                         f"prefill paired {n_heads}/{n_kv} n {n_tokens} start {start}")
+            start += n_tokens
+    finally:
+        be_gpu.close()
+
+
 @pytest.mark.parametrize("n_heads,n_kv,tiles,persistent", [(16, 2, 2, 0), (16, 2, 3, 1),
                                                            (8, 4, 3, 0), (8, 4, 2, 1)])
 def test_dev_prefill_key_chunks_groups(monkeypatch, n_heads, n_kv, tiles, persistent):

@@ -26,3 +26,20 @@ def test_prefill_workspace_budget(tmp_path):
                    check=True, capture_output=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
+def test_prefill_paired_plans(tmp_path):
+    """Paired 16-query plans (bnr::plan_prefill_pairs) over 1600 seeded
+    shapes: key-tile coverage, chunk order, bins of at most two pieces within
+    tau, the grid mapping, disjoint partial-state slots within the budget,
+    and the stack shape's 51 bins of at most 21 key tiles (host only)."""
+    _lib.load()
+    lib_dir = os.path.dirname(_lib.LIB_PATH)
+    exe = tmp_path / "prefill_pair_check"
+    subprocess.run([HIPCC, "-O1", "-std=c++17", "-I", os.path.join(ROOT, "bitnetrs_amd", "csrc"),
+                    "-o", str(exe), os.path.join(ROOT, "tests", "native", "prefill_pair_check.cpp"),
+                    "-L", lib_dir, "-lbitnet_hip", f"-Wl,-rpath,{lib_dir}"],
+                   check=True, capture_output=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.startswith("ok"), out.stdout + out.stderr
