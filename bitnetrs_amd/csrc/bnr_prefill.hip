@@ -219,7 +219,6 @@ template <int G>
 __device__ __forceinline__ floatx16 pf_tile_s_copy(const float *dk, const float (&qf)[64],
                                                    const PrefillArgs &a, int h, int ktn,
                                                    float *nk, float *nv) {
-  constexpr int NI = kPrefillTile / 4 / (64 * G);
   const int lane = threadIdx.x & 63, hl = lane >> 5, col = lane & 31;
   floatx16 S = floatx16{};
   const float *krow = dk + col * kHeadDim + 64 * hl;
@@ -509,7 +508,6 @@ template <int G>
 __device__ __forceinline__ void pf16_tile_s_copy(const float *dk, const float (&qf)[32],
                                                  const PrefillArgs &a, int h, int ktn, float *nk,
                                                  float *nv, floatx4 &S0, floatx4 &S1) {
-  constexpr int NI = kPrefillTile / 4 / (64 * G);  // copies per wave per half tile
   const int lane = threadIdx.x & 63, j = lane & 15, u = lane >> 4;
   // K rows j and 16 + j; chunk c of a row sits at chunk c ^ (row % 16) = c ^ j
   const float *k0 = dk + j * kHeadDim, *k1 = dk + (16 + j) * kHeadDim;
@@ -548,6 +546,19 @@ __device__ __forceinline__ void pf16_tile_pv(const PrefillArgs &a, int q0h, int 
                                              float &m, float &l) {
   const int lane = threadIdx.x & 63, j = lane & 15, u = lane >> 4;
   const int kbase = kt * 32;
+  // The tile's V fragments, all read before the softmax: V row of PV step
+  // st is key 16 (st/4) + 4u + st%4.  (Read one step ahead instead, the
+  // next step's registers are the current step's, so each read waits for
+  // the products before it and each step then waits for its reads.)
+  const float *v0 = dv + 4 * u * kHeadDim + 4 * j;
+  float4 va[8], vb[8];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    const float *vr = v0 + (16 * (st >> 2) + (st & 3)) * kHeadDim;
+    va[st] = ld4(vr);
+    vb[st] = ld4(vr + 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float s[8] = {S0[0], S0[1], S0[2], S0[3], S1[0], S1[1], S1[2], S1[3]};  // key 16(i/4) + 4u + i%4
   if (kbase + 31 > a.start_pos + q0h) {  // the tile reaches the causal diagonal
     const int pq = a.start_pos + min(q0h + j, a.n_tokens - 1);
@@ -574,26 +585,16 @@ __device__ __forceinline__ void pf16_tile_pv(const PrefillArgs &a, int q0h, int 
     ls += p[i];
   }
   l += ls;  // this lane's keys; the query's sum spans its four lanes
-  // V row of PV step st: key 16 (st/4) + 4u + st%4; each step's two reads
-  // are issued one step ahead of their products.
-  const float *v0 = dv + 4 * u * kHeadDim + 4 * j;
-  float4 na = ld4(v0), nb = ld4(v0 + 64);
 #pragma unroll
   for (int st = 0; st < 8; ++st) {
-    const float4 va = na, vb = nb;
-    if (st < 7) {
-      const float *vr = v0 + (16 * ((st + 1) >> 2) + ((st + 1) & 3)) * kHeadDim;
-      na = ld4(vr);
-      nb = ld4(vr + 64);
-    }
-    O[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.x, p[st], O[0], 0, 0, 0);
-    O[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.y, p[st], O[1], 0, 0, 0);
-    O[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.z, p[st], O[2], 0, 0, 0);
-    O[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(va.w, p[st], O[3], 0, 0, 0);
-    O[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.x, p[st], O[4], 0, 0, 0);
-    O[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.y, p[st], O[5], 0, 0, 0);
-    O[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.z, p[st], O[6], 0, 0, 0);
-    O[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb.w, p[st], O[7], 0, 0, 0);
+    O[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[st].x, p[st], O[0], 0, 0, 0);
+    O[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[st].y, p[st], O[1], 0, 0, 0);
+    O[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[st].z, p[st], O[2], 0, 0, 0);
+    O[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[st].w, p[st], O[3], 0, 0, 0);
+    O[4] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[st].x, p[st], O[4], 0, 0, 0);
+    O[5] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[st].y, p[st], O[5], 0, 0, 0);
+    O[6] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[st].z, p[st], O[6], 0, 0, 0);
+    O[7] = __builtin_amdgcn_mfma_f32_16x16x4f32(vb[st].w, p[st], O[7], 0, 0, 0);
   }
 }
 
@@ -746,6 +747,8 @@ void prefill16_kernel(PrefillArgs a) {
       __builtin_amdgcn_s_barrier();
     }
     pf16_tile_pv(a, q0h, kt, S0, S1, dv, O, m, l);
+    // the wait for the next tile's copies stays after the products
+    __builtin_amdgcn_sched_barrier(0);
     wait_vmem();
     __syncthreads();
   };
