@@ -459,18 +459,20 @@ PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu
 // Paired plan of a 16-query launch that fits one dispatch round: the key
 // tiles of every 16-query unit (queries 16 u .. 16 u + 15 attend key tiles
 // 0 .. nk(u) - 1) are cut into pieces and the pieces packed into at most
-// min(n_cu / n_kv, kMaxPairBins) bins of at most two pieces and tau key
-// tiles each, tau as small as the packing allows.  piece[2 b + s] is piece
-// s of bin b (s = 0 the longer one, started first):
+// min(n_cu / n_kv, kMaxPairBins) bins of at most two pieces each, packed so
+// that the slowest CU of a model of two workgroups sharing it finishes
+// early.  piece[2 b + s] is piece s of bin b (s = 0 the longer one, started
+// first):
 //   w0 = kt0 | qt << 16 | half << 31        (unit u = 2 qt + half)
 //   w1 = len | ch << 8 | nch << 16 | base << 24
 // with len = 0 for an empty slot.  The chunks of a unit are its pieces in
 // key order; a query tile's split units use slots base .. base + nch - 1
-// (n_slots per kv head).  `span` is the modelled span in prefill_span's
-// units.
+// (n_slots per kv head).  tau is the largest bin's key tiles, `span` the
+// modelled span in prefill_span's units, model_us the largest bin's time in
+// the planner's CU model of two workgroups (us).
 struct PairPlan {
   int bins = 0, tau = 0, n_slots = 0;
-  double span = 0.0;
+  double span = 0.0, model_us = 0.0;
   unsigned piece[2 * kMaxPairBins][2] = {};
 };
 bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long long item_budget,

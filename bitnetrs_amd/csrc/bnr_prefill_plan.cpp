@@ -226,14 +226,147 @@ bool pair_pack(const std::vector<int> &nk, int tau, int thr, int max_bins,
   return true;
 }
 
+// Time (us) of a CU running one bin: pieces of a and b key tiles (a >= b,
+// b = 0 for none), split units (sa, sb) ending with a partial state and a
+// ticket.  The first-dispatched workgroup has issue priority: side by side
+// it runs a tile in kTileOld, the other in kTileYoung; alone either runs one
+// in kTileAlone; the second's end phase is slower while the first still
+// runs.  Fitted to per-workgroup timelines of paired 1024-token launches
+// (16-query halves, 20/5 heads, MI355X; within 1.2 us over 20 bin shapes).
+constexpr double kStartOld = 3.5, kStartYoung = 4.9, kTileOld = 3.70, kTileYoung = 5.66,
+                 kTileAlone = 2.50, kEndUnsplit = 0.8, kEndSplit = 2.6,
+                 kEndYoungUnsplit = 2.7, kEndYoungSplit = 4.5;
+double bin_time(int a, int b, bool sa, bool sb) {
+  const double ea = sa ? kEndSplit : kEndUnsplit;
+  if (b == 0) return kStartOld + a * kTileAlone + ea;
+  const double ty = kStartYoung + b * kTileYoung, to = kStartOld + a * kTileOld;
+  if (ty <= to) {
+    const double done = (ty - kStartOld) / kTileOld;
+    return std::max(ty + (sb ? kEndYoungSplit : kEndYoungUnsplit), ty + (a - done) * kTileAlone + ea);
+  }
+  const double done = (to - kStartYoung) / kTileYoung;
+  return std::max(to + ea, to + (b - done) * kTileAlone + (sb ? kEndSplit : kEndUnsplit));
+}
+
+// The largest modelled bin time of a packing (a unit is split when it has
+// more than one piece).
+double packing_time(const std::vector<PairBin> &bins, int nu) {
+  std::vector<int> pieces((size_t)nu, 0);
+  for (const PairBin &b : bins)
+    for (int k = 0; k < b.n; ++k) ++pieces[(size_t)b.p[k].unit];
+  double worst = 0.0;
+  for (const PairBin &b : bins) {
+    if (b.n == 0) continue;
+    const bool first = b.n < 2 || b.p[0].len >= b.p[1].len;
+    const PairPiece &x = first ? b.p[0] : b.p[1];
+    const PairPiece *y = b.n < 2 ? nullptr : first ? &b.p[1] : &b.p[0];
+    worst = std::max(worst, bin_time(x.len, y ? y->len : 0, pieces[(size_t)x.unit] > 1,
+                                     y && pieces[(size_t)y->unit] > 1));
+  }
+  return worst;
+}
+
+// Packing for a target bin time Ts under bin_time.  Repeatedly, the
+// shortest remaining unit (or remainder) that can go beside another piece is
+// the bin's second piece, whole, and the first piece is the longest the
+// model allows beside it (a remainder of exactly that length, else cut from
+// the longest -- or, with !largest, the shortest longer -- remainder);
+// once every remainder is too long to go second, bins take the most key
+// tiles the model allows as two cut pieces, the first from the longest
+// remainder, the second from the shortest.  False when the bins exceed
+// max_bins or a piece cannot meet Ts.
+bool model_pack(const std::vector<int> &nk, double Ts, int max_bins, bool largest,
+                std::vector<PairBin> &bins) {
+  bins.clear();
+  auto amax = [&](int b, bool sa, bool sb) {
+    int a = -1;
+    for (int x = std::max(b, 1); x <= 255; ++x) {
+      if (bin_time(x, b, sa, sb) > Ts) break;
+      a = x;
+    }
+    return a;
+  };
+  // the longest first piece beside a whole second piece of b tiles
+  std::vector<int> A;
+  for (int b = 0; b <= 255; ++b) {
+    A.push_back(amax(b, true, false));
+    if (A.back() < b) break;
+  }
+  int ymax = 0;
+  for (int b = 1; b <= 255 && amax(b, true, true) >= b; ++b) ymax = b;
+  int bal_a = amax(0, true, false), bal_b = 0;
+  for (int b = 1; b <= ymax; ++b) {
+    const int a = amax(b, true, true);
+    if (a + b > bal_a + bal_b) {
+      bal_a = a;
+      bal_b = b;
+    }
+  }
+  if (bal_a < 1) return false;
+  struct Entry {
+    int size, unit, kt0;
+    bool whole;
+  };
+  std::vector<Entry> pool;
+  for (int u = 0; u < (int)nk.size(); ++u) pool.push_back(Entry{nk[(size_t)u], u, 0, true});
+  auto take = [](Entry &e, int n) {
+    const PairPiece pc{e.unit, e.kt0, n};
+    e.size -= n;
+    e.kt0 += n;
+    e.whole = false;
+    return pc;
+  };
+  for (;;) {
+    pool.erase(std::remove_if(pool.begin(), pool.end(), [](const Entry &e) { return e.size <= 0; }),
+               pool.end());
+    if (pool.empty()) return true;
+    if ((int)bins.size() >= max_bins) return false;
+    std::sort(pool.begin(), pool.end(), [](const Entry &x, const Entry &y) {
+      return x.size != y.size ? x.size < y.size : x.unit < y.unit;
+    });
+    PairBin bin{};
+    if (pool[0].size <= ymax) {
+      const int a = pool[0].size < (int)A.size() ? A[(size_t)pool[0].size] : -1;
+      if (a < pool[0].size) return false;
+      const PairPiece young = take(pool[0], pool[0].size);
+      size_t pick = 0;  // 0: none
+      for (size_t i = 1; i < pool.size() && !pick; ++i)
+        if (pool[i].size == a) pick = i;
+      if (!pick) {
+        for (size_t i = 1; i < pool.size(); ++i)
+          if (pool[i].size > a && (!pick || (largest ? pool[i].size > pool[pick].size
+                                                      : pool[i].size < pool[pick].size)))
+            pick = i;
+      }
+      if (!pick && pool.size() > 1) pick = pool.size() - 1;  // the longest, whole
+      if (pick) {
+        bin.p[bin.n++] = take(pool[pick], std::min(a, pool[pick].size));
+      }
+      bin.p[bin.n++] = young;
+    } else {
+      Entry &L = pool.back();
+      bin.p[bin.n++] = take(L, std::min(bal_a, L.size));
+      Entry *e = nullptr;
+      for (Entry &x : pool)
+        if (x.size > 0 && (!e || x.size < e->size)) e = &x;
+      if (e && bal_b > 0) bin.p[bin.n++] = take(*e, std::min(bal_b, e->size));
+    }
+    bin.sum = bin.p[0].len + (bin.n > 1 ? bin.p[1].len : 0);
+    bins.push_back(bin);
+  }
+}
+
 }  // namespace
 
-// The paired plan (see PairPlan).  For each tau from the mean bin load up,
-// every threshold between pairing whole units and cutting the chain is
-// packed, the packing with the fewest pieces kept; the first tau whose
-// packing fits the bins and the partial-state slots wins.  Its span is
-// prefill_span's CU model applied to each bin: the two pieces side by side,
-// the longer finishing alone, plus the merge of a split unit.
+// The paired plan (see PairPlan).  Two packings compete under bin_time:
+// the chain packing (for each tau from the mean bin load up, every
+// threshold between pairing whole units and cutting the chain is packed,
+// the one with the fewest pieces kept, the first tau that fits the bins and
+// the partial-state slots taken) and model_pack at the smallest target
+// (0.1 us steps from the balanced bin's time) it meets.  The faster one in
+// the model is encoded; `span` is prefill_span's CU model applied to its
+// bins: the two pieces side by side, the longer finishing alone, plus the
+// merge of a split unit.
 bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long long item_budget,
                         PairPlan &p) {
   p = PairPlan{};
@@ -249,7 +382,29 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
     nk[(size_t)u] = (int)(std::min<long long>(start_pos + 16LL * u + 15, last_row) / 32 + 1);
     S += nk[(size_t)u];
   }
-  std::vector<PairBin> bins, best;
+  const int nqt = (n_tokens + 31) / 32;
+  // Slots of the split query tiles (both halves share a slot index); false
+  // past the budget.
+  auto slots = [&](const std::vector<PairBin> &bins, std::vector<int> &nch, std::vector<int> &base,
+                   int &n_slots) {
+    nch.assign((size_t)nu, 0);
+    for (const PairBin &b : bins)
+      for (int k = 0; k < b.n; ++k) ++nch[(size_t)b.p[k].unit];
+    base.assign((size_t)nqt, 0);
+    n_slots = 0;
+    for (int qt = 0; qt < nqt; ++qt) {
+      const int m = std::max(nch[(size_t)(2 * qt)], 2 * qt + 1 < nu ? nch[(size_t)(2 * qt + 1)] : 0);
+      base[(size_t)qt] = n_slots;
+      if (m > 1) n_slots += m;
+    }
+    for (int v : nch)
+      if (v > 255) return false;
+    return n_slots <= 256 && (long long)n_slots * n_kv <= item_budget;
+  };
+  std::vector<int> nch, base;
+  int n_slots = 0;
+  // the chain packing
+  std::vector<PairBin> bins, chain, model;
   std::vector<int> thr;
   for (int tau = (int)std::max<long long>(1, (S + max_bins - 1) / max_bins); tau <= 255; ++tau) {
     thr.assign({1, tau + 1});
@@ -258,7 +413,7 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
     std::sort(thr.begin(), thr.end());
     thr.erase(std::unique(thr.begin(), thr.end()), thr.end());
     int best_pieces = 1 << 30;
-    best.clear();
+    std::vector<PairBin> best;
     for (int t : thr) {
       if (!pair_pack(nk, tau, t, max_bins, bins)) continue;
       int pieces = 0;
@@ -268,52 +423,70 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
         best = bins;
       }
     }
-    if (best.empty()) continue;
-    // chunks of each unit in key order
-    std::vector<int> nch((size_t)nu, 0);
-    for (const PairBin &b : best)
-      for (int k = 0; k < b.n; ++k) ++nch[(size_t)b.p[k].unit];
-    // slots of the split query tiles (both halves share a slot index)
-    const int nqt = (n_tokens + 31) / 32;
-    std::vector<int> base((size_t)nqt, 0);
-    int n_slots = 0;
-    for (int qt = 0; qt < nqt; ++qt) {
-      const int m = std::max(nch[(size_t)(2 * qt)], 2 * qt + 1 < nu ? nch[(size_t)(2 * qt + 1)] : 0);
-      base[(size_t)qt] = n_slots;
-      if (m > 1) n_slots += m;
+    if (!best.empty() && slots(best, nch, base, n_slots)) {
+      chain = best;
+      break;
     }
-    if (n_slots > 256 || (long long)n_slots * n_kv > item_budget) continue;
-    p.bins = (int)best.size();
-    p.tau = tau;
-    p.n_slots = n_slots;
-    double span = 0.0;
-    constexpr double kShared = 1.9;
-    for (size_t b = 0; b < best.size(); ++b) {
-      PairBin bin = best[b];
-      if (bin.n == 2 && bin.p[1].len > bin.p[0].len) std::swap(bin.p[0], bin.p[1]);
-      double w[2] = {0.0, 0.0}, tail = 0.0;
-      for (int k = 0; k < bin.n; ++k) {
-        const PairPiece &pc = bin.p[k];
-        const int u = pc.unit, qt = u / 2, half = u & 1;
-        int ch = 0;  // pieces of the unit before this one
-        for (const PairBin &o : best)
-          for (int j = 0; j < o.n; ++j)
-            if (o.p[j].unit == u && o.p[j].kt0 < pc.kt0) ++ch;
-        const int n = nch[(size_t)u];
-        p.piece[2 * b + k][0] = (unsigned)pc.kt0 | (unsigned)qt << 16 | (unsigned)half << 31;
-        p.piece[2 * b + k][1] = (unsigned)pc.len | (unsigned)ch << 8 | (unsigned)n << 16 |
-                                (unsigned)(n > 1 ? base[(size_t)qt] : 0) << 24;
-        w[k] = g_pf16_fixed + pc.len * g_pf16_tile;
-        if (n > 1) tail = std::max(tail, (n - 1) * g_pf16_merge);
-      }
-      const double a = std::min(w[0], w[1]), c = std::max(w[0], w[1]);
-      span = std::max(span, (bin.n == 2 ? a * kShared + (c - a) : c) + tail);
-    }
-    p.span = span;
-    return true;
   }
-  p = PairPlan{};
-  return false;
+  const double t_chain = chain.empty() ? 1e300 : packing_time(chain, nu);
+  // the model packing, at most as slow as the chain's: 1 us steps from
+  // below the balanced bin's time to the first target met, then 0.1 us steps
+  // over the last 1 us
+  {
+    auto attempt = [&](double ts) {
+      for (int largest = 1; largest >= 0; --largest) {
+        if (!model_pack(nk, ts, max_bins, largest != 0, bins)) continue;
+        if (packing_time(bins, nu) > ts + 1e-9 || !slots(bins, nch, base, n_slots)) continue;
+        model = bins;
+        return true;
+      }
+      return false;
+    };
+    const int mean = (int)((S + max_bins - 1) / max_bins);
+    const double t0 = bin_time((mean * 3 + 4) / 5, mean - (mean * 3 + 4) / 5, true, true) - 2.0;
+    const double t_end = std::min(t_chain, t0 + 1000.0);
+    double hit = -1.0;
+    for (double ts = t0; ts < t_end + 1.0 && hit < 0; ts += 1.0)
+      if (attempt(std::min(ts, t_end))) hit = std::min(ts, t_end);
+    for (int i = 1; hit >= 0 && i < 10; ++i)
+      if (!attempt(hit - 1.0 + 0.1 * i)) continue;
+      else break;
+  }
+  const std::vector<PairBin> *pick = nullptr;
+  if (!model.empty() && packing_time(model, nu) < t_chain) pick = &model;
+  else if (!chain.empty()) pick = &chain;
+  if (!pick) return false;
+  const std::vector<PairBin> &best = *pick;
+  slots(best, nch, base, n_slots);
+  p.bins = (int)best.size();
+  p.n_slots = n_slots;
+  p.model_us = packing_time(best, nu);
+  double span = 0.0;
+  constexpr double kShared = 1.9;
+  for (size_t b = 0; b < best.size(); ++b) {
+    PairBin bin = best[b];
+    if (bin.n == 2 && bin.p[1].len > bin.p[0].len) std::swap(bin.p[0], bin.p[1]);
+    p.tau = std::max(p.tau, bin.p[0].len + (bin.n > 1 ? bin.p[1].len : 0));
+    double w[2] = {0.0, 0.0}, tail = 0.0;
+    for (int k = 0; k < bin.n; ++k) {
+      const PairPiece &pc = bin.p[k];
+      const int u = pc.unit, qt = u / 2, half = u & 1;
+      int ch = 0;  // pieces of the unit before this one
+      for (const PairBin &o : best)
+        for (int j = 0; j < o.n; ++j)
+          if (o.p[j].unit == u && o.p[j].kt0 < pc.kt0) ++ch;
+      const int n = nch[(size_t)u];
+      p.piece[2 * b + k][0] = (unsigned)pc.kt0 | (unsigned)qt << 16 | (unsigned)half << 31;
+      p.piece[2 * b + k][1] = (unsigned)pc.len | (unsigned)ch << 8 | (unsigned)n << 16 |
+                              (unsigned)(n > 1 ? base[(size_t)qt] : 0) << 24;
+      w[k] = g_pf16_fixed + pc.len * g_pf16_tile;
+      if (n > 1) tail = std::max(tail, (n - 1) * g_pf16_merge);
+    }
+    const double a = std::min(w[0], w[1]), c = std::max(w[0], w[1]);
+    span = std::max(span, (bin.n == 2 ? a * kShared + (c - a) : c) + tail);
+  }
+  p.span = span;
+  return true;
 }
 
 // The chunk size, balance and query height for a prefill shape.  Each
