@@ -227,29 +227,31 @@ bool pair_pack(const std::vector<int> &nk, int tau, int thr, int max_bins,
 }
 
 // Time (us) of a CU running one bin: pieces of a and b key tiles (a >= b,
-// b = 0 for none), split units (sa, sb) ending with a partial state and a
-// ticket.  The first-dispatched workgroup has issue priority: side by side
-// it runs a tile in kTileOld, the other in kTileYoung; alone either runs one
-// in kTileAlone; the second's end phase is slower while the first still
-// runs.  Fitted to per-workgroup timelines of paired 1024-token launches
-// (16-query halves, 20/5 heads, MI355X; within 1.2 us over 20 bin shapes).
-constexpr double kStartOld = 3.5, kStartYoung = 4.9, kTileOld = 3.70, kTileYoung = 5.66,
-                 kTileAlone = 2.50, kEndUnsplit = 0.8, kEndSplit = 2.6,
-                 kEndYoungUnsplit = 2.7, kEndYoungSplit = 4.5;
-double bin_time(int a, int b, bool sa, bool sb) {
-  const double ea = sa ? kEndSplit : kEndUnsplit;
-  if (b == 0) return kStartOld + a * kTileAlone + ea;
+// b = 0 for none) of units cut into na and nb pieces (1: unsplit; a split
+// piece ends with a partial state and a ticket, the unit's last one with
+// the merge).  The first-dispatched workgroup has issue priority: side by
+// side it runs a tile in kTileOld, the other in kTileYoung; alone either
+// runs one in kTileAlone; the second's end phase is slower while the first
+// still runs.  Least-squares fit to the per-CU finish times of 46 bin
+// shapes in per-workgroup timelines of paired 1024-token launches (16-query
+// halves, 20/5 heads, MI355X): 0.52 us rms, 1.3 us at most.
+constexpr double kStartOld = 3.272, kStartYoung = 4.6, kTileOld = 3.926, kTileYoung = 5.388,
+                 kTileAlone = 2.53, kEndUnsplit = 0.85, kEndSplit = 1.808, kEndSplit3 = 2.135,
+                 kEndYoungUnsplit = 4.018, kEndYoungSplit = 6.063;
+double bin_time(int a, int b, int na, int nb) {
+  auto end = [](int n) { return n <= 1 ? kEndUnsplit : n == 2 ? kEndSplit : kEndSplit3; };
+  if (b == 0) return kStartOld + a * kTileAlone + end(na);
   const double ty = kStartYoung + b * kTileYoung, to = kStartOld + a * kTileOld;
   if (ty <= to) {
     const double done = (ty - kStartOld) / kTileOld;
-    return std::max(ty + (sb ? kEndYoungSplit : kEndYoungUnsplit), ty + (a - done) * kTileAlone + ea);
+    return std::max(ty + (nb <= 1 ? kEndYoungUnsplit : kEndYoungSplit),
+                    ty + (a - done) * kTileAlone + end(na));
   }
   const double done = (to - kStartYoung) / kTileYoung;
-  return std::max(to + ea, to + (b - done) * kTileAlone + (sb ? kEndSplit : kEndUnsplit));
+  return std::max(to + end(na), to + (b - done) * kTileAlone + end(nb));
 }
 
-// The largest modelled bin time of a packing (a unit is split when it has
-// more than one piece).
+// The largest modelled bin time of a packing.
 double packing_time(const std::vector<PairBin> &bins, int nu) {
   std::vector<int> pieces((size_t)nu, 0);
   for (const PairBin &b : bins)
@@ -260,8 +262,8 @@ double packing_time(const std::vector<PairBin> &bins, int nu) {
     const bool first = b.n < 2 || b.p[0].len >= b.p[1].len;
     const PairPiece &x = first ? b.p[0] : b.p[1];
     const PairPiece *y = b.n < 2 ? nullptr : first ? &b.p[1] : &b.p[0];
-    worst = std::max(worst, bin_time(x.len, y ? y->len : 0, pieces[(size_t)x.unit] > 1,
-                                     y && pieces[(size_t)y->unit] > 1));
+    worst = std::max(worst, bin_time(x.len, y ? y->len : 0, pieces[(size_t)x.unit],
+                                     y ? pieces[(size_t)y->unit] : 1));
   }
   return worst;
 }
@@ -278,10 +280,12 @@ double packing_time(const std::vector<PairBin> &bins, int nu) {
 bool model_pack(const std::vector<int> &nk, double Ts, int max_bins, bool largest,
                 std::vector<PairBin> &bins) {
   bins.clear();
+  // cut pieces counted as two-way splits (a unit cut more often is caught
+  // by the caller's packing_time check)
   auto amax = [&](int b, bool sa, bool sb) {
     int a = -1;
     for (int x = std::max(b, 1); x <= 255; ++x) {
-      if (bin_time(x, b, sa, sb) > Ts) break;
+      if (bin_time(x, b, sa ? 2 : 1, sb ? 2 : 1) > Ts) break;
       a = x;
     }
     return a;
@@ -443,7 +447,7 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
       return false;
     };
     const int mean = (int)((S + max_bins - 1) / max_bins);
-    const double t0 = bin_time((mean * 3 + 4) / 5, mean - (mean * 3 + 4) / 5, true, true) - 2.0;
+    const double t0 = bin_time((mean * 3 + 4) / 5, mean - (mean * 3 + 4) / 5, 2, 2) - 2.0;
     const double t_end = std::min(t_chain, t0 + 1000.0);
     double hit = -1.0;
     for (double ts = t0; ts < t_end + 1.0 && hit < 0; ts += 1.0)
