@@ -222,9 +222,11 @@ struct PrefillArgs {
   // (kv head, query tile, half).
   int q16;
   // Paired launch of the 16-query kernel (pair_bins > 0, q16 = 1): a 1-D grid
-  // of 2 * pair_cu workgroups.  Workgroup i runs piece i / pair_cu of bin
-  // b = (i % pair_cu) / n_kv for kv head (i % pair_cu) % n_kv; a bin past
-  // pair_bins or a piece of zero length exits at once.  A piece is a key
+  // of 2 * pair_cu workgroups.  Workgroup i runs piece i / pair_cu on CU
+  // c = i % pair_cu, renumbered XCD by XCD when pair_cu % 8 == 0:
+  // c' = (c % 8) (pair_cu / 8) + c / 8 (else c' = c); c' is bin c' % pair_bins
+  // of kv head c' / pair_bins.  A head past n_kv or a piece of zero length
+  // exits at once.  A piece is a key
   // range of one 16-query unit (pf16_pair_piece has the encoding); the plan
   // puts at most two pieces in a bin so that they share a CU: on an idle
   // device the dispatcher gives workgroups i and i + (CU count) the same CU,

@@ -676,12 +676,16 @@ __device__ __forceinline__ void pf16_finish(const PrefillArgs &a, const PfItem &
 // false for a workgroup past the plan's bins or on an empty slot.
 __device__ __forceinline__ bool pf16_pair_piece(const PrefillArgs &a, PfItem &it, int &half) {
   const int cu = (int)blockIdx.x % a.pair_cu, slot = (int)blockIdx.x / a.pair_cu;
-  const int bin = cu / a.n_kv;
-  if (bin >= a.pair_bins) return false;
+  // CUs numbered XCD by XCD (workgroup i runs on XCD i % 8) and a kv head's
+  // bins on consecutive ones, so that an XCD's L2 holds the K/V of at most
+  // two heads (5 heads on 8 XCDs) rather than of every head.
+  const int cux = (a.pair_cu & 7) == 0 ? (cu & 7) * (a.pair_cu >> 3) + (cu >> 3) : cu;
+  const int hh = cux / a.pair_bins, bin = cux - hh * a.pair_bins;
+  if (hh >= a.n_kv) return false;
   const unsigned w0 = a.pair_piece[2 * bin + slot][0], w1 = a.pair_piece[2 * bin + slot][1];
   const int len = (int)(w1 & 255u);
   if (len == 0) return false;
-  it.h = cu - bin * a.n_kv;
+  it.h = hh;
   it.y = 2 * bin + slot;
   it.kt0 = (int)(w0 & 0xFFFFu);
   it.nkt = it.kt0 + len;

@@ -48,8 +48,10 @@ bool check(int n, int start, int n_kv, int n_cu, long long budget, const PairPla
   // the kernel's grid mapping reaches each (bin, piece, kv head) once
   std::vector<int> seen((size_t)pl.bins * 2 * n_kv, 0);
   for (int i = 0; i < 2 * n_cu; ++i) {
-    const int cu = i % n_cu, slot = i / n_cu, bin = cu / n_kv, h = cu % n_kv;
-    if (bin >= pl.bins) continue;
+    const int cu = i % n_cu, slot = i / n_cu;
+    const int cux = n_cu % 8 == 0 ? (cu % 8) * (n_cu / 8) + cu / 8 : cu;
+    const int h = cux / pl.bins, bin = cux % pl.bins;
+    if (h >= n_kv) continue;
     ++seen[((size_t)bin * 2 + slot) * n_kv + h];
   }
   for (int v : seen)
@@ -132,7 +134,7 @@ int main() {
   }
   std::mt19937 rng(20261202);
   const int kvs[] = {1, 2, 3, 5, 8};
-  const int cus[] = {80, 256};
+  const int cus[] = {80, 256, 100};
   for (int n_cu : cus) {
     for (int n_kv : kvs) {
       for (int r = 0; r < 160; ++r) {
