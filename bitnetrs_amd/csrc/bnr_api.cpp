@@ -1678,14 +1678,13 @@ bool prefill_tiled(size_t n_tokens, size_t start_pos, size_t n_heads, size_t n_k
 }
 
 // Stream-K where every query tile has about as many keys as the next (a
-// cached prefix at least as long as the new tokens) and the tokens are more
-// than 512: 1024 after 3000 305 us against 316 us for the planned 16-query
-// chunks and 312 us for 32-query ones, 1024 after 1024 155 us against 147-
-// 154 us (MI355X, graph-timed).  Planned chunks otherwise -- from an empty
-// cache (N = 1024: 62 vs 85 us, N = 4096: 671 vs 710 us) and for short
-// launches after a long prefix, where the 16-query kernel wins (512 after
-// 512: 48 vs 61 us, 256 after 1024: 38 vs 56 us).
-bool prefill_streamk(const bnr_ctx *c, size_t n_tokens, size_t start_pos) {
+// cached prefix at least as long as the new tokens, which are more than 512)
+// and no paired launch is planned, or the prefix is at least twice as long:
+// 1024 after 3000 303 us against 316 us for a paired launch; 1024 after
+// 1024 153 us against 150 us paired (MI355X, graph-timed).  Chunked or paired
+// launches otherwise (N = 1024 from an empty cache: 54-62 vs 85 us, 4096:
+// 671 vs 710 us).
+bool prefill_streamk_shape(const bnr_ctx *c, size_t n_tokens, size_t start_pos) {
   return c->pf_chunk_tiles <= 0 &&
          (c->pf_mode == kPrefillStreamK ||
           (c->pf_mode == kPrefillAuto && start_pos >= n_tokens && n_tokens > 512));
@@ -1715,7 +1714,11 @@ int prefill_attention_locked(bnr_ctx *c, const float *q, const float *k_cache,
     pa.n_qtiles = (int)((n_tokens + 31) / 32);
     pa.timeline = c->timeline;
     const int per_cu = group >= 8 ? 1 : 2;  // resident workgroups per CU (registers, LDS)
-    const bool streamk = prefill_streamk(c, n_tokens, start_pos);
+    bool streamk = prefill_streamk_shape(c, n_tokens, start_pos);
+    if (streamk && c->pf_mode == kPrefillAuto && start_pos < 2 * n_tokens)
+      streamk = !plan_prefill_cached(c, (int)n_tokens, (int)start_pos, (int)n_kv_heads, group,
+                                     (long long)cap)
+                     .choice.pairs;
     int pair_slots = -1;  // a paired launch: its partial-state slots per kv head
     if (!streamk) {
       if (c->pf_chunk_tiles > 0) {

@@ -451,8 +451,9 @@ struct PrefillChoice {
   int tiles, balanced, q16;
   int pairs;  // a paired 16-query launch (PairPlan) instead of chunks
 };
-// bal_pref / q16_pref / pair_pref: -1 either, 0 never, 1 always (a paired
-// launch where one is possible; its plan goes to *pairs).
+// bal_pref / q16_pref: -1 either, 0 never, 1 always.  pair_pref != 0 (with
+// q16_pref != 0 and pairs given): a paired launch wherever one fits, its
+// plan in *pairs.
 struct PairPlan;
 PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
                                  int q16_pref, long long cap, int pair_pref = 0,
@@ -482,7 +483,7 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
 // Constants of the 16-query halves in the span model (fixed cost, key tile,
 // merge per extra chunk; a 32-query tile alone on a CU takes 1) and the
 // span ratio below which the planner switches to them.
-extern double g_pf16_fixed, g_pf16_tile, g_pf16_merge, g_pf16_margin, g_pair_margin;
+extern double g_pf16_fixed, g_pf16_tile, g_pf16_merge, g_pf16_margin;
 long long prefill_item_budget(long long cap, int n_kv);
 constexpr long long kPrefillMaxPlannedItems = 8192;
 // persistent_wgs > 0: that many resident workgroups take items from a.queue.

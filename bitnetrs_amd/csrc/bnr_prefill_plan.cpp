@@ -160,13 +160,6 @@ double prefill_span(int n_tokens, int start_pos, int n_kv, int ctiles_in, int n_
 
 constexpr int kPrefillChunkCandidates[] = {3, 4, 5, 6, 7, 8, 10, 12, 14, 16, 20, 24, 32, 48, 64};
 
-// Span ratio below which the planner takes a paired launch.  The bin model
-// overrates the pairs' span: graph-timed on MI355X (20/5 heads) they beat
-// the planned chunks where the modelled ratio is up to 1.03 (512 tokens
-// 24.4 vs 26.0 us, 1536 tokens 114.5 vs 120.5 us, 768 tokens 37.2 vs 41.7
-// us, 1024 tokens 57.8-58.1 vs 59.5-60.7 us) and lose by 2 % at 1.023 (256
-// after 1024 cached rows).
-double g_pair_margin = 1.03;
 
 namespace {
 
@@ -504,6 +497,14 @@ bool plan_prefill_pairs(int n_tokens, int start_pos, int n_kv, int n_cu, long lo
 PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu, int bal_pref,
                                  int q16_pref, long long cap, int pair_pref, PairPlan *pairs) {
   const long long budget = prefill_item_budget(cap, n_kv);
+  // A paired launch (one dispatch round of the 16-query kernel) wherever one
+  // fits: graph-timed on MI355X (20/5 heads) it matches or beats the planned
+  // chunks at every shape tried -- 256 to 1536 tokens from an empty cache
+  // (1024: 53.6 vs 60.0 us, 768: 35.6 vs 42.2 us) and after cached prefixes
+  // (512 after 512: 45.2 vs 47.9 us, 300 after 5: 16.6 vs 17.7 us).
+  if (pairs && pair_pref != 0 && q16_pref != 0 &&
+      plan_prefill_pairs(n_tokens, start_pos, n_kv, n_cu, budget, *pairs))
+    return PrefillChoice{kPrefillNoSplit, 0, 1, 1};
   PrefillChoice best{kPrefillNoSplit, 0, 0, 0};
   double best_span = 1e300;
   for (int q = 0; q <= 1; ++q) {
@@ -528,14 +529,6 @@ PrefillChoice plan_prefill_chunk(int n_tokens, int start_pos, int n_kv, int n_cu
         }
       }
     }
-  }
-  // A paired launch: one dispatch round of the 16-query kernel.
-  PairPlan pp;
-  if (pairs && pair_pref != 0 && q16_pref != 0 &&
-      plan_prefill_pairs(n_tokens, start_pos, n_kv, n_cu, budget, pp) &&
-      (pair_pref == 1 || pp.span < best_span * g_pair_margin)) {
-    *pairs = pp;
-    best = PrefillChoice{kPrefillNoSplit, 0, 1, 1};
   }
   return best;
 }
