@@ -1066,7 +1066,8 @@ def prefill_launch_stats(rows, tick_us):
     """One launch's records (rows of 8 words, one per workgroup) -> phase
     statistics in us: span, start latency, per-key-tile time, partial-state
     store + ticket, merge, output store; per-CU residency and how many
-    workgroups are still running as the launch drains."""
+    workgroups are still running as the launch drains; and per CU, the
+    (key tiles, chunks) of its workgroups in entry order with its end."""
     import numpy as np
 
     t0 = rows[:, PF_ENTRY].min()
@@ -1122,7 +1123,15 @@ def prefill_launch_stats(rows, tick_us):
     # workgroups still running at tenths of the span
     out["running_by_tenth"] = [int(((rows[:, PF_ENTRY] <= t0 + f * span) & (ends > t0 + f * span)).sum())
                                for f in np.arange(0.0, 1.0, 0.1)]
-    return out, t0, ends.max()
+    # what each CU ran: its workgroups' (key tiles, chunks of their query
+    # unit) in the order they entered, and when its last one ended
+    bins = []
+    for c in cus:
+        sel = np.nonzero(cu_key == c)[0]
+        sel = sel[np.argsort(rows[sel, PF_ENTRY], kind="stable")]
+        bins.append((tuple((int(ntiles[j]), int(nch[j])) for j in sel),
+                     float(ends[sel].max() - t0) * tick_us))
+    return out, bins, t0, ends.max()
 
 
 def prefill_timeline_main(args) -> int:
@@ -1178,7 +1187,7 @@ def prefill_timeline_main(args) -> int:
     tick_us = 1.0 / 100.0
     t0e = torch.cuda.Event(enable_timing=True)
     t1e = torch.cuda.Event(enable_timing=True)
-    samples, gaps, per_layer = [], [], []
+    samples, gaps, per_layer, cu_bins = [], [], [], {}
     for r in range(reps):
         qp.copy_(q_in)
         kp.copy_(k_in)
@@ -1193,8 +1202,10 @@ def prefill_timeline_main(args) -> int:
         bounds = []
         for i in range(n_layers):
             rows = st[i][st[i][:, PF_ENTRY] != 0]
-            stats, first, last = prefill_launch_stats(rows, tick_us)
+            stats, bins, first, last = prefill_launch_stats(rows, tick_us)
             samples.append(stats)
+            for comp, end in bins:
+                cu_bins.setdefault(comp, []).append(end)
             bounds.append((first, last))
         gaps += [(bounds[i + 1][0] - bounds[i][1]) * tick_us for i in range(n_layers - 1)]
     med = lambda xs: float(np.median(xs))  # noqa: E731
@@ -1211,6 +1222,11 @@ def prefill_timeline_main(args) -> int:
             res[key if key in ("wgs", "cus", "key_tiles_mean", "cu_tile_busy", "cu_residents")
                 else key + "_us"] = round(med([x[key] for x in samples]), 3)
     res["span_tflops"] = round(flops / (res["span_us"] * 1e-6) / 1e12, 2)
+    # the CU workloads that end last: [(key tiles, chunks) per workgroup in
+    # entry order], CUs per launch running it, median end (us from launch start)
+    slow = sorted(cu_bins.items(), key=lambda kv: -np.median(kv[1]))[:10]
+    res["cu_bins_slowest"] = [[[list(w) for w in comp], round(len(ends) / len(samples), 2),
+                               round(med(ends), 2)] for comp, ends in slow]
     print(json.dumps(res), flush=True)
     be.close()
     return 0
