@@ -194,14 +194,12 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
 // the same scale as norm_quant_kernel would; the int8 vector never leaves
 // LDS.  The workgroup issues the (cache-resident) activation loads first and
 // its weight loads right after, so the prologue runs under the weights'
-// latency.  K <= 8192 (one LDS pass); workgroup 0 writes h_out
-// (mode residual), which must not alias a or b.
+// latency.  K <= 4096 NG (one LDS pass; NG = 1 or 2 16-activation groups
+// per thread, the smallest that holds K, so that K <= 4096 keeps the
+// registers of one group: 4 resident workgroups per CU instead of 3);
+// workgroup 0 writes h_out (mode residual), which must not alias a or b.
 // ---------------------------------------------------------------------------
 constexpr int kNormK = 8192;
-constexpr int kNormGroups = kNormK / 16;     // 16-activation groups
-constexpr int kNormPieces = kNormK / 64;     // 16-byte weight pieces per row
-constexpr int kNormPiecesPerLane = kNormPieces / 16;
-constexpr int kNormGroupsPerThread = kNormGroups / 256;
 
 // x from the glue inputs: a | a + b | max(a, 0)^2 * b (mode kGlue*).
 __device__ __forceinline__ float norm_x_of(int mode, float u, float v) {
@@ -240,10 +238,13 @@ __device__ __forceinline__ float norm_y(float x, float inv, float g) {
   return x * inv * g;
 }
 
-template <bool VEC>
+template <bool VEC, int NG>
 __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroupArgs a,
                                                                 GemvNormArgs p) {
-  __shared__ uint4 s_act[kNormGroups];
+  constexpr int kNormGroupsPerThread = NG;
+  constexpr int kNormPieces = 64 * NG;  // 16-byte weight pieces per row (K <= 4096 NG)
+  constexpr int kNormPiecesPerLane = kNormPieces / 16;
+  __shared__ uint4 s_act[256 * NG];
   __shared__ float red[4];
   const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15, lane = tid & 63, wv_id = tid >> 6;
   const int b = blockIdx.x;
@@ -414,10 +415,15 @@ hipError_t launch_ternary_gemv_norm(const TernaryGemvGroupArgs &a, const GemvNor
   const int wgs = a.wg_off[a.n];
   if (wgs <= 0) return hipSuccess;
   if (a.in_features > kNormK) return hipErrorInvalidValue;
-  if (vec)
-    ternary_gemv_norm_kernel<true><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  const bool one = a.in_features <= kNormK / 2;
+  if (vec && one)
+    ternary_gemv_norm_kernel<true, 1><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  else if (vec)
+    ternary_gemv_norm_kernel<true, 2><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  else if (one)
+    ternary_gemv_norm_kernel<false, 1><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
   else
-    ternary_gemv_norm_kernel<false><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+    ternary_gemv_norm_kernel<false, 2><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
   return hipGetLastError();
 }
 

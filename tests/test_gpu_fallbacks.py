@@ -44,10 +44,12 @@ def host(t):
 
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
-@pytest.mark.parametrize("k,offset", [(2560, False), (2560, True), (100, False), (1000, False)])
+@pytest.mark.parametrize("k,offset", [(2560, False), (2560, True), (100, False), (1000, False),
+                                      (4096, False), (4112, False), (6912, True)])
 def test_norm_fused_gemv_paths(backend, mode, k, offset):
     """bnr_dev_ternary_gemv_norm_group against the oracle's norm -> quantise
-    -> ternary GEMV, for two matrices with row counts that end mid-workgroup.
+    -> ternary GEMV, for two matrices with row counts that end mid-workgroup
+    (K up to 4096 takes one 16-activation group per thread, longer K two).
     The sum of squares is a tree on the GPU, so an int8 activation may sit
     one step away where y*127/max falls on a half: each such flip moves an
     output by at most one step of its combined scale."""
