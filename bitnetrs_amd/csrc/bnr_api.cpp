@@ -278,6 +278,9 @@ struct bnr_ctx {
   int pf_sk_wgs = 0;              // stream-K workgroups (0: every resident slot)
   int pf_q16 = -1;                // 16-query halves (prefill16_kernel): -1 planner, 0 never, 1 always
   int pf_balanced = -1;           // balanced key chunks: -1 planner, 0 never, 1 always
+  // norm-fused GEMV: the most rows per workgroup (16, 32, 64) that keep the
+  // launch at or above this many workgroups
+  int gemv_norm_min_wgs = 256;
   int pf_pair = -1;               // paired 16-query launches: -1 planner (4 q heads per kv head), 0 never, 1 where possible
   std::vector<PrefillPlanEntry> pf_plans;  // recent (shape -> key tiles per chunk) plans
 };
@@ -903,6 +906,7 @@ extern "C" int bnr_create(int device_id, bnr_ctx **out) {
   if (const char *v = std::getenv("BNR_PREFILL_SK_WGS")) c->pf_sk_wgs = std::max(atoi(v), 0);
   if (const char *v = std::getenv("BNR_PREFILL_Q16")) c->pf_q16 = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_BALANCED")) c->pf_balanced = std::min(1, std::max(-1, atoi(v)));
+  if (const char *v = std::getenv("BNR_GEMV_NORM_MIN_WGS")) c->gemv_norm_min_wgs = std::max(1, atoi(v));
   if (const char *v = std::getenv("BNR_PREFILL_PAIR")) c->pf_pair = std::min(1, std::max(-1, atoi(v)));
   if (const char *v = std::getenv("BNR_PREFILL_MODE")) {
     const int m = atoi(v);
@@ -2070,6 +2074,18 @@ extern "C" int bnr_dev_ternary_gemv_norm_group(
   g.in_features = (int)in_features;
   g.packed_cols = (long long)((in_features + 3) / 4);
   bool vec = g.packed_cols % 16 == 0;
+  // Rows per workgroup: each workgroup reads all of a (and b) and gamma, so
+  // the launch takes the most rows per workgroup that still leave it
+  // gemv_norm_min_wgs workgroups.
+  int rows = 16;
+  for (int r : {64, 32}) {
+    long long w = 0;
+    for (size_t i = 0; i < n; ++i) w += ((long long)out_features[i] + r - 1) / r;
+    if (w >= c->gemv_norm_min_wgs) {
+      rows = r;
+      break;
+    }
+  }
   int wgs = 0;
   for (size_t i = 0; i < n; ++i) {
     int st = check_gemv(SIZE_MAX, weight_scales[i], SIZE_MAX, 1.0f, SIZE_MAX, out_features[i],
@@ -2082,7 +2098,7 @@ extern "C" int bnr_dev_ternary_gemv_norm_group(
     g.weight_scale[i] = weight_scales[i];
     g.out_features[i] = (int)out_features[i];
     g.wg_off[i] = wgs;
-    wgs += (int)((out_features[i] + 15) / 16);
+    wgs += (int)((out_features[i] + rows - 1) / rows);
     vec = vec && ((uintptr_t)weight_packed[i] % 16) == 0;
   }
   for (size_t i = n; i <= (size_t)kMaxGemvGroup; ++i) g.wg_off[i] = wgs;
@@ -2094,6 +2110,7 @@ extern "C" int bnr_dev_ternary_gemv_norm_group(
   p.gamma = gamma;
   p.eps = eps;
   p.h_out = mode == BNR_GLUE_RESIDUAL ? h_out : nullptr;
+  p.rows = rows;
   // The vector path also reads the activation vectors as float4 groups.
   vec = vec && in_features % 16 == 0 && aligned16(a) && aligned16(gamma) &&
         (mode == BNR_GLUE_PLAIN || aligned16(b)) && (!p.h_out || aligned16(p.h_out));

@@ -76,6 +76,15 @@ __device__ __forceinline__ int row_sum16_i(int v) {
   v += dpp_i<0x140>(v);  // row_mirror
   return v;
 }
+// Sum over aligned groups of L = 4, 8 or 16 lanes, in the group's first lane.
+template <int L>
+__device__ __forceinline__ int lane_group_sum_i(int v) {
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  if (L >= 8) v += dpp_i<0x141>(v);
+  if (L >= 16) v += dpp_i<0x140>(v);
+  return v;
+}
 
 // Bytes [off, off+16) of p, the ones at or past `limit` read as zero.
 __device__ __forceinline__ uint4 load16_bounded(const uint8_t *p, long long off, long long limit) {
@@ -198,6 +207,9 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
 // per thread, the smallest that holds K, so that K <= 4096 keeps the
 // registers of one group: 4 resident workgroups per CU instead of 3);
 // workgroup 0 writes h_out (mode residual), which must not alias a or b.
+// A workgroup owns 256 / LPR rows, LPR lanes per row: every workgroup reads
+// the whole of a (and b) and gamma, so a launch with many rows takes 32 or
+// 64 rows per workgroup to read those vectors fewer times.
 // ---------------------------------------------------------------------------
 constexpr int kNormK = 8192;
 
@@ -238,15 +250,16 @@ __device__ __forceinline__ float norm_y(float x, float inv, float g) {
   return x * inv * g;
 }
 
-template <bool VEC, int NG>
+template <bool VEC, int NG, int LPR>
 __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroupArgs a,
                                                                 GemvNormArgs p) {
   constexpr int kNormGroupsPerThread = NG;
   constexpr int kNormPieces = 64 * NG;  // 16-byte weight pieces per row (K <= 4096 NG)
-  constexpr int kNormPiecesPerLane = kNormPieces / 16;
+  constexpr int kNormPiecesPerLane = kNormPieces / LPR;
+  constexpr int kRows = 256 / LPR;
   __shared__ uint4 s_act[256 * NG];
   __shared__ float red[4];
-  const int tid = threadIdx.x, slot = tid >> 4, j = tid & 15, lane = tid & 63, wv_id = tid >> 6;
+  const int tid = threadIdx.x, slot = tid / LPR, j = tid % LPR, lane = tid & 63, wv_id = tid >> 6;
   const int b = blockIdx.x;
   const uint8_t *w = a.weight[0];
   float *out = a.out[0];
@@ -263,7 +276,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
     }
   }
   const int K = a.in_features, nb = (K + 3) / 4;
-  const int row = (b - off) * kRowsPerWg + slot;
+  const int row = (b - off) * kRows + slot;
   const long long b0 = (long long)min(row, m - 1) * a.packed_cols;
   // 1. x for groups tid, tid+256 (16 consecutive elements each) and gamma,
   // loaded before the weights: loads return in order, so these small,
@@ -294,7 +307,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
   uint4 wq[kNormPiecesPerLane];
 #pragma unroll
   for (int i = 0; i < kNormPiecesPerLane; ++i) {
-    const int c = j + 16 * i;
+    const int c = j + LPR * i;
     if (VEC)
       wq[i] = 16 * c < nb ? *reinterpret_cast<const uint4 *>(w + b0 + 16 * c) : make_uint4(0, 0, 0, 0);
     else
@@ -393,7 +406,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
   int acc = 0;
 #pragma unroll
   for (int i = 0; i < kNormPiecesPerLane; ++i) {
-    const int c = j + 16 * i;
+    const int c = j + LPR * i;
     if (16 * c < nb) {
       acc = dot16(wq[i].x, s_act[c], acc);
       acc = dot16(wq[i].y, s_act[kNormPieces + c], acc);
@@ -401,7 +414,7 @@ __global__ __launch_bounds__(256) void ternary_gemv_norm_kernel(TernaryGemvGroup
       acc = dot16(wq[i].w, s_act[3 * kNormPieces + c], acc);
     }
   }
-  acc = row_sum16_i(acc);
+  acc = lane_group_sum_i<LPR>(acc);
   // combined_scale = weight_scale * act_scale / 127.0 (gemv.rs:297), act_scale = scale * 127
   const float t = ws * (scale * 127.0f);
   const float cs = t / 127.0f;
@@ -416,14 +429,22 @@ hipError_t launch_ternary_gemv_norm(const TernaryGemvGroupArgs &a, const GemvNor
   if (wgs <= 0) return hipSuccess;
   if (a.in_features > kNormK) return hipErrorInvalidValue;
   const bool one = a.in_features <= kNormK / 2;
-  if (vec && one)
-    ternary_gemv_norm_kernel<true, 1><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
-  else if (vec)
-    ternary_gemv_norm_kernel<true, 2><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
-  else if (one)
-    ternary_gemv_norm_kernel<false, 1><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
-  else
-    ternary_gemv_norm_kernel<false, 2><<<dim3(wgs), dim3(256), 0, s>>>(a, p);
+  auto go = [&](auto kern) { kern<<<dim3(wgs), dim3(256), 0, s>>>(a, p); };
+  switch (p.rows) {
+    case 16:
+      if (vec) one ? go(ternary_gemv_norm_kernel<true, 1, 16>) : go(ternary_gemv_norm_kernel<true, 2, 16>);
+      else one ? go(ternary_gemv_norm_kernel<false, 1, 16>) : go(ternary_gemv_norm_kernel<false, 2, 16>);
+      break;
+    case 32:
+      if (vec) one ? go(ternary_gemv_norm_kernel<true, 1, 8>) : go(ternary_gemv_norm_kernel<true, 2, 8>);
+      else one ? go(ternary_gemv_norm_kernel<false, 1, 8>) : go(ternary_gemv_norm_kernel<false, 2, 8>);
+      break;
+    case 64:
+      if (vec) one ? go(ternary_gemv_norm_kernel<true, 1, 4>) : go(ternary_gemv_norm_kernel<true, 2, 4>);
+      else one ? go(ternary_gemv_norm_kernel<false, 1, 4>) : go(ternary_gemv_norm_kernel<false, 2, 4>);
+      break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -577,6 +577,7 @@ struct GemvNormArgs {
   const float *a, *b, *gamma;
   float eps;
   float *h_out;  // mode residual: a + b, written by workgroup 0; must not alias a or b
+  int rows;      // rows per workgroup: 16, 32 or 64 (wg_off counts workgroups of that many)
 };
 constexpr int kMaxNormGemvK = 8192;
 hipError_t launch_ternary_gemv_norm(const TernaryGemvGroupArgs &a, const GemvNormArgs &p, bool vec,

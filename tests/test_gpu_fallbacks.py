@@ -47,13 +47,27 @@ def host(t):
 @pytest.mark.parametrize("k,offset", [(2560, False), (2560, True), (100, False), (1000, False),
                                       (4096, False), (4112, False), (6912, True)])
 def test_norm_fused_gemv_paths(backend, mode, k, offset):
+    _norm_fused_gemv_case(backend, mode, k, offset, [40, 23])
+
+
+@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("k", [2560, 6912])
+@pytest.mark.parametrize("rows", [[5000, 3300], [9000, 7400]])
+def test_norm_fused_gemv_rows_per_workgroup(backend, mode, k, rows):
+    """As test_norm_fused_gemv_paths with matrices large enough that the
+    launch takes 32 rows per workgroup (5000 + 3300 rows) or 64 (9000 + 7400
+    rows), both ending mid-workgroup."""
+    _norm_fused_gemv_case(backend, mode, k, False, rows)
+
+
+def _norm_fused_gemv_case(backend, mode, k, offset, rows):
     """bnr_dev_ternary_gemv_norm_group against the oracle's norm -> quantise
     -> ternary GEMV, for two matrices with row counts that end mid-workgroup
     (K up to 4096 takes one 16-activation group per thread, longer K two).
     The sum of squares is a tree on the GPU, so an int8 activation may sit
     one step away where y*127/max falls on a half: each such flip moves an
     output by at most one step of its combined scale."""
-    case(f"norm-fused gemv mode {mode} k {k} offset {offset}")
+    case(f"norm-fused gemv mode {mode} k {k} offset {offset} rows {rows}")
     import torch
 
     import bitnetrs_amd
@@ -74,7 +88,6 @@ def test_norm_fused_gemv_paths(backend, mode, k, offset):
     oracle.rms_norm(x, g, 1e-5, y)
     q, s = oracle.absmax_quantize_row(y)
     act_absmax = float(f32(s) * f32(127.0))
-    rows = [40, 23]
     scales = [0.05, 0.03]
     mats = [oracle.pack_rows(rng.integers(-1, 2, size=(m, k)).astype(np.int8)) for m in rows]
     refs = []
