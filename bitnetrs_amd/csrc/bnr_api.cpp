@@ -140,7 +140,28 @@ struct Mirror {
   size_t rows = 0;    // rows per kv head held on the device
   size_t synced = 0;  // rows 0..synced-1 match the host
   float *dk = nullptr, *dv = nullptr;
+  std::vector<float> probe;  // kv_probe of the host rows at the last sync
 };
+
+// Samples of rows 0, (n-1)/2 and n-1 of every kv head of a host cache: the
+// first and last four floats of the k and v rows.  Taken when a mirror is
+// synced to n rows; the next call uploads only its new row if they still
+// match, and re-uploads every row if one of them was rewritten since.  A
+// rewrite of any other row goes unseen and needs bnr_mirror_invalidate.
+void kv_probe(const float *k, const float *v, size_t n_kv, size_t head_stride, size_t head_dim,
+              size_t n, std::vector<float> &out) {
+  out.clear();
+  if (n == 0) return;
+  const size_t c = std::min<size_t>(4, head_dim);
+  const size_t rows[3] = {0, (n - 1) / 2, n - 1};
+  for (size_t kh = 0; kh < n_kv; ++kh)
+    for (size_t r : rows)
+      for (const float *src : {k, v}) {
+        const float *row = src + kh * head_stride + r * head_dim;
+        out.insert(out.end(), row, row + c);
+        out.insert(out.end(), row + head_dim - c, row + head_dim);
+      }
+}
 
 // HBM copy of one host ternary weight matrix, for bnr_ternary_gemv_preq.
 // The fingerprint (64 bytes sampled across the buffer) catches a different
@@ -247,6 +268,7 @@ struct bnr_ctx {
 
   // mirrors, most recently used first
   std::list<Mirror> mirrors;
+  std::vector<float> probe_now;  // kv_probe scratch (capacity kept across calls)
   std::list<WeightMirror> weight_mirrors;
   uint8_t *d_bytes = nullptr;  // int8 activation staging
   size_t d_bytes_n = 0;
@@ -1059,7 +1081,12 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     m = &c->mirrors.front();
   }
   size_t r0 = 0;
-  if (c->mirror_mode == BNR_MIRROR_INCREMENTAL && m->synced == cur_pos) r0 = cur_pos;
+  if (c->mirror_mode == BNR_MIRROR_INCREMENTAL && m->synced == cur_pos) {
+    kv_probe(k_cache, v_cache, n_kv_heads, head_stride, head_dim, cur_pos, c->probe_now);
+    if (c->probe_now.size() == m->probe.size() &&
+        std::memcmp(c->probe_now.data(), m->probe.data(), m->probe.size() * sizeof(float)) == 0)
+      r0 = cur_pos;
+  }
   if (r0 == cur_pos && cur_pos > 0 && fast_shape(n_heads, n_kv_heads, head_dim)) {
     // One new row: the decode kernel reads q and row cur_pos of every kv
     // head from the zero-copy staging, appends the row to the mirror itself
@@ -1098,6 +1125,7 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
     if (st) return st;
     std::memcpy(output, h + in_n, out_len * sizeof(float));
     m->synced = seq_len;
+    kv_probe(k_cache, v_cache, n_kv_heads, head_stride, head_dim, seq_len, m->probe);
     return set_ok();
   }
   const size_t dpitch = m->rows * head_dim * sizeof(float);
@@ -1111,6 +1139,7 @@ extern "C" int bnr_masked_attention(bnr_ctx *c, const float *q, size_t q_len,
                            n_kv_heads, hipMemcpyHostToDevice, c->stream),
           "mirror upload v");
   m->synced = seq_len;
+  kv_probe(k_cache, v_cache, n_kv_heads, head_stride, head_dim, seq_len, m->probe);
 
   int st = ensure_buf(&c->d_q, &c->d_q_n, q_len, "staging alloc");
   if (st) return st;

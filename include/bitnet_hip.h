@@ -100,9 +100,11 @@ int bnr_rope_embed(bnr_ctx *ctx, float *q, size_t q_len, float *k, size_t k_len,
  * cap is k_len / n_kv_heads / head_dim, as in the reference (attention.rs:
  * 128).  The context keeps an HBM mirror of each host cache, keyed by
  * (k_cache, v_cache, k_len): when the mirror holds exactly rows
- * 0..cur_pos-1, only row cur_pos is uploaded; otherwise rows 0..=cur_pos
- * are re-uploaded.  Validation order and error kinds follow attention.rs:
- * 109-161. */
+ * 0..cur_pos-1, and rows 0, (cur_pos-1)/2 and cur_pos-1 still begin and end
+ * with the floats they held when the mirror was synced (4 of each k and v
+ * row of every kv head are compared), only row cur_pos is uploaded;
+ * otherwise rows 0..=cur_pos are re-uploaded.  Validation order and error
+ * kinds follow attention.rs:109-161. */
 int bnr_masked_attention(bnr_ctx *ctx, const float *q, size_t q_len, const float *k_cache,
                          size_t k_len, const float *v_cache, size_t v_len, float *output,
                          size_t out_len, size_t n_heads, size_t n_kv_heads,
@@ -112,7 +114,8 @@ int bnr_masked_attention(bnr_ctx *ctx, const float *q, size_t q_len, const float
 #define BNR_MIRROR_INCREMENTAL 0 /* upload only the new row when in sync (default) */
 #define BNR_MIRROR_FULL 1        /* upload rows 0..=cur_pos on every call          */
 int bnr_set_mirror_mode(bnr_ctx *ctx, int mode);
-/* Forget every mirror (call after rewriting rows other than the newest). */
+/* Forget every mirror (call after rewriting cached rows in place: the
+ * samples above catch rewrites of the three sampled rows only). */
 int bnr_mirror_invalidate(bnr_ctx *ctx);
 
 /* Run-to-run reproducible decode, no counterpart in the reference (whose CPU

@@ -161,6 +161,28 @@ def test_host_mirror_incremental_decode(backend, n_heads, n_kv, hd):
     assert_close(out, out_ref, "rewind")
 
 
+@pytest.mark.parametrize("row", ["first", "middle", "last"])
+def test_host_mirror_sampled_rewrite_resyncs(backend, row):
+    """A cached row rewritten in place without bnr_mirror_invalidate: when it
+    is one of the rows the mirror samples at each sync (0, (n-1)/2, n-1 of
+    the n synced rows), the next call re-uploads every row and matches the
+    oracle on the rewritten cache."""
+    case(f"host mirror: in-place rewrite of the {row} synced row")
+    backend.mirror_invalidate()
+    w = decode_workload(32, 100, cap=128)
+    kc, vc = w["k_cache"].reshape(-1), w["v_cache"].reshape(-1)
+    q = w["q"]
+    out = np.zeros(HQ * D, f32)
+    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 99)  # synced to rows 0..99
+    r = {"first": 0, "middle": 49, "last": 99}[row]
+    kc[r * D:(r + 1) * D] += 3.0  # kv head 0's row r: its first and last floats change
+    vc[(2 * 128 + r) * D:(2 * 128 + r + 1) * D] -= 2.0  # kv head 2's row r
+    ref = np.zeros_like(out)
+    oracle.masked_attention(q, kc, vc, ref, HQ, HKV, D, 100)
+    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 100)
+    assert_close(out, ref, f"{row} row rewritten")
+
+
 def test_host_mirror_invalidate_and_full_mode(backend):
     case("host mirror invalidate / full mode")
     import bitnetrs_amd
