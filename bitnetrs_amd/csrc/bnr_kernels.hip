@@ -130,6 +130,12 @@ __global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) 
       st4(dst + i + half, hi);
     }
   };
+  // the v row first: its loads go out with the q/k loads instead of after
+  // their stores (which they could alias)
+  constexpr int F = kHeadDim / 4;  // float4 per row
+  const bool has_v = a.v_cache && t < a.n_kv * F;
+  float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (has_v) vv = ld4_nt(a.v + ((long long)tok * a.n_kv + t / F) * kHeadDim + 4 * (t % F));
   const float4 c = ld4(a.cos_tab + (long long)pos * half + i);
   const float4 sn = ld4(a.sin_tab + (long long)pos * half + i);
   for (int h = t >> 4; h < nrot; h += 32) {
@@ -145,9 +151,9 @@ __global__ __launch_bounds__(256) void rope_append_row_kernel(RopeAppendArgs a) 
     finish(h, x1, lo, hi);
     if (h2 < nrot) finish(h2, x2, lo2, hi2);
   }
+  if (has_v) st4(a.v_cache + (t / F) * a.kv_stride + (long long)pos * kHeadDim + 4 * (t % F), vv);
   if (a.v_cache) {
-    constexpr int F = kHeadDim / 4;  // float4 per row
-    for (int f = t; f < a.n_kv * F; f += 256) {
+    for (int f = t + 256; f < a.n_kv * F; f += 256) {  // n_kv > 8 only
       const int hv = f / F, j = 4 * (f % F);
       const float4 v = ld4_nt(a.v + ((long long)tok * a.n_kv + hv) * kHeadDim + j);
       st4(a.v_cache + hv * a.kv_stride + (long long)pos * kHeadDim + j, v);
