@@ -215,8 +215,8 @@ __global__ __launch_bounds__(256) void ternary_gemv_group_kernel(TernaryGemvGrou
 // LDS.  The workgroup issues the (cache-resident) activation loads first and
 // its weight loads right after, so the prologue runs under the weights'
 // latency.  K <= 4096 NG (one LDS pass; NG = 1 or 2 16-activation groups
-// per thread, the smallest that holds K, so that K <= 4096 keeps the
-// registers of one group: 4 resident workgroups per CU instead of 3);
+// per thread, the smallest that holds K: at K <= 4096 the kernel needs 74
+// VGPRs and 6 workgroups fit a CU, with two groups 142 and 3);
 // workgroup 0 writes h_out (mode residual), which must not alias a or b.
 // A workgroup owns 256 / LPR rows, LPR lanes per row: every workgroup reads
 // the whole of a (and b) and gamma, so a launch with many rows takes 32 or
