@@ -115,14 +115,26 @@ def _norm_fused_gemv_case(backend, mode, k, offset, rows):
 
 @pytest.mark.parametrize("head_dim,offset", [(12, False), (128, True), (128, False), (64, False)])
 def test_rope_append_paths(backend, head_dim, offset):
+    _rope_append_case(backend, head_dim, offset, 4, 2)
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 16), (32, 16), (40, 20)])
+def test_rope_append_many_kv_heads(backend, nh, nkv):
+    """As test_rope_append_paths at head_dim 128 with more than 8 kv heads: the
+    v rows of a token then take more than one float4 per thread, and with
+    more than 32 rotated heads the head loop a second pass."""
+    _rope_append_case(backend, 128, False, nh, nkv)
+
+
+def _rope_append_case(backend, head_dim, offset, nh, nkv):
     """bnr_dev_rope_append for 5 tokens at positions 7..11: q and k rotated in
     place and the cache rows written, bit for bit against the oracle's
     rope_embed and KVCache::store_kv."""
-    case(f"rope_append head_dim {head_dim} offset {offset}")
+    case(f"rope_append head_dim {head_dim} offset {offset} heads {nh}/{nkv}")
     import torch
 
-    nh, nkv, n, start, cap = 4, 2, 5, 7, 16
-    rng = np.random.default_rng(900 + head_dim + offset)
+    n, start, cap = 5, 7, 16
+    rng = np.random.default_rng(900 + head_dim + offset + 1000 * nkv)
     q = rng.standard_normal((n, nh * head_dim)).astype(f32)
     k = rng.standard_normal((n, nkv * head_dim)).astype(f32)
     v = rng.standard_normal((n, nkv * head_dim)).astype(f32)
