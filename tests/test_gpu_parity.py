@@ -162,24 +162,28 @@ def test_host_mirror_incremental_decode(backend, n_heads, n_kv, hd):
 
 
 @pytest.mark.parametrize("row", ["first", "middle", "last"])
-def test_host_mirror_sampled_rewrite_resyncs(backend, row):
+@pytest.mark.parametrize("n_heads,n_kv,hd", [(HQ, HKV, D), (4, 2, 2), (6, 3, 16)])
+def test_host_mirror_sampled_rewrite_resyncs(backend, row, n_heads, n_kv, hd):
     """A cached row rewritten in place without bnr_mirror_invalidate: when it
     is one of the rows the mirror samples at each sync (0, (n-1)/2, n-1 of
-    the n synced rows), the next call re-uploads every row and matches the
-    oracle on the rewritten cache."""
-    case(f"host mirror: in-place rewrite of the {row} synced row")
+    the n synced rows; min(4, head_dim) floats at each end of a row), the
+    next call re-uploads every row and matches the oracle on the rewritten
+    cache."""
+    case(f"host mirror: in-place rewrite of the {row} synced row, heads {n_heads}/{n_kv} d {hd}")
     backend.mirror_invalidate()
-    w = decode_workload(32, 100, cap=128)
+    cap = 128
+    w = decode_workload(32, 100, cap=cap, n_heads=n_heads, n_kv=n_kv, head_dim=hd)
     kc, vc = w["k_cache"].reshape(-1), w["v_cache"].reshape(-1)
     q = w["q"]
-    out = np.zeros(HQ * D, f32)
-    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 99)  # synced to rows 0..99
+    out = np.zeros(n_heads * hd, f32)
+    backend.masked_attention(q, kc, vc, out, n_heads, n_kv, hd, 99)  # synced to rows 0..99
     r = {"first": 0, "middle": 49, "last": 99}[row]
-    kc[r * D:(r + 1) * D] += 3.0  # kv head 0's row r: its first and last floats change
-    vc[(2 * 128 + r) * D:(2 * 128 + r + 1) * D] -= 2.0  # kv head 2's row r
+    kc[r * hd:(r + 1) * hd] += 3.0  # kv head 0's row r: its first and last floats change
+    h2 = n_kv - 1
+    vc[(h2 * cap + r) * hd:(h2 * cap + r + 1) * hd] -= 2.0  # the last kv head's row r
     ref = np.zeros_like(out)
-    oracle.masked_attention(q, kc, vc, ref, HQ, HKV, D, 100)
-    backend.masked_attention(q, kc, vc, out, HQ, HKV, D, 100)
+    oracle.masked_attention(q, kc, vc, ref, n_heads, n_kv, hd, 100)
+    backend.masked_attention(q, kc, vc, out, n_heads, n_kv, hd, 100)
     assert_close(out, ref, f"{row} row rewritten")
 
 
